@@ -1,0 +1,184 @@
+/*
+ * moba_hip.h -- C ABI of the MI355X (gfx950) MoBA block-sparse attention
+ * library `libmoba_hip.so`.
+ *
+ * One entry point per stage of the reference's hot path
+ * (ZuricZ/moba-triton, paths relative to the reference root):
+ *
+ *   pool -> gate -> CSC transpose -> KV-block-major attend -> LSE merge
+ *   delta -> KV-block-major backward (dK, dV, per-slot dQ) -> dQ reduce
+ *
+ * Conventions (same as the reference, src/moba/gqa.py:55-62):
+ *   - API tensors are token-major [B, S, H, D] (packed: [1, T, H, D]).
+ *   - Internal buffers are head-major: kbar [R, Hkv, nb, D], block ids
+ *     [B, Hq, S, slots], partials [B, Hq, S, slots(, D)], lse/delta
+ *     [B, Hq, S]. R = B, or the sequence count when packed.
+ *   - All pointers are device pointers allocated by the caller; nothing in
+ *     this library allocates device memory. Scratch comes in through the
+ *     `workspace` arguments, sized by the *_workspace_size queries.
+ *   - Every call is asynchronous on `stream` (a hipStream_t, NULL = default
+ *     stream) and never synchronises with the host.
+ *   - Return value: MOBA_OK or an error code; moba_last_error() gives the
+ *     message of the last failure on the calling thread. Shape / config
+ *     errors are MOBA_ERR_INVALID (the Python layer raises ValueError, as
+ *     the reference's _validate does, src/moba/kernels/moba_fwd.py:733-780);
+ *     unsupported dtype / head_dim combinations are MOBA_ERR_UNSUPPORTED.
+ *   - cu_seqlens (int32 [n_seq + 1], device) selects packed mode when
+ *     non-NULL; then `batch` is the sequence count, `seq_len` the packed
+ *     token count T, and `max_seqlen` the longest sequence.
+ */
+#ifndef MOBA_HIP_H_
+#define MOBA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum moba_status {
+  MOBA_OK = 0,
+  MOBA_ERR_INVALID = 1,
+  MOBA_ERR_UNSUPPORTED = 2,
+  MOBA_ERR_LAUNCH = 3,
+  MOBA_ERR_WORKSPACE = 4
+};
+
+enum moba_dtype { MOBA_BF16 = 0, MOBA_FP16 = 1, MOBA_FP32 = 2 };
+
+/* Library identity. */
+int moba_abi_version(void);
+const char* moba_last_error(void);
+const char* moba_status_string(int status);
+
+/*
+ * Block means of K: kbar[r, h, n, :] = dtype( dtype(sum) / occupancy ).
+ * Replaces pool_blocks (src/moba/kernels/pooling.py:103-163) and its kernel
+ * (pooling.py:26-96). The block sum is exact (float64), then rounded to
+ * float32 and to the input dtype before the divide; the quotient is rounded
+ * to the input dtype. A short tail block divides by its real count.
+ * k: [B, S, Hkv, D]; kbar: [R, Hkv, n_blocks, D]. Packed: blocks never
+ * cross sequence boundaries and rows beyond a sequence's own block count are
+ * left untouched.
+ */
+int moba_pool(const void* k, void* kbar, const int32_t* cu_seqlens,
+              int64_t batch, int64_t seq_len, int64_t max_seqlen,
+              int64_t h_kv, int64_t head_dim, int64_t n_blocks,
+              int64_t block_size, int dtype, void* stream);
+
+/*
+ * Gate: per query, the own block (if `always_current`) plus the top `take`
+ * strictly-past blocks by q . kbar (unscaled), ranked by (score desc, block
+ * id asc), score = exact dot rounded to float32 then to the input dtype.
+ * Emits ids ascending, -1 padded: block_idx [B, Hq, S, slots] int32.
+ * Replaces gate_select (src/moba/kernels/gating.py:343-448) and gate_kernel
+ * (gating.py:93-335); selection semantics of src/moba/naive.py:64-146.
+ * Under GQA query head g reads kbar head g / (Hq / Hkv).
+ */
+size_t moba_gate_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q);
+int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
+              const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+              int64_t max_seqlen, int64_t h_q, int64_t h_kv,
+              int64_t head_dim, int64_t n_blocks, int64_t block_size,
+              int64_t slots, int64_t take, int always_current, int dtype,
+              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * CSC transpose of block_idx into per-(row, kv head, block) columns:
+ * col_nnz [R, Hkv, nb], col_offsets [R, Hkv, nb + 1] (exclusive prefix
+ * sum), row_indices / head_indices / slot_of_pair [R, Hkv, cap] with
+ * cap = (Hq / Hkv) * rows_per_seq * slots, order [R, Hkv, nb] (column ids by
+ * count desc, id asc). Entries claim their position within a column with
+ * an atomic cursor, so their order inside a column is unspecified (as in the
+ * reference, routing.py:35-52); each (query, slot) pair appears exactly
+ * once. row_indices hold packed token indices when cu_seqlens is given.
+ * Replaces build_csc_from_indices (src/moba/kernels/routing.py:309-427)
+ * and its three kernels (routing.py:139-301); CSCIndex fields of
+ * routing.py:73-130.
+ */
+size_t moba_csc_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q,
+                               int64_t h_kv, int64_t n_blocks,
+                               int64_t slots);
+int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
+                   int32_t* col_offsets, int32_t* row_indices,
+                   int32_t* head_indices, int32_t* slot_of_pair,
+                   int32_t* order, const int32_t* cu_seqlens, int64_t batch,
+                   int64_t seq_len, int64_t max_seqlen, int64_t h_q,
+                   int64_t h_kv, int64_t n_blocks, int64_t slots,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * KV-block-major attend: for every column, the keys of that block against
+ * every query that selected it; writes per-slot un-normalised partials
+ * part_m (row max of q.k * D^-1/2 * log2 e, log2 units), part_l (sum of
+ * exp2), part_acc (sum of exp2 * v, in acc_dtype). Unwritten slots keep
+ * part_m = -inf, which this call sets before the kernel runs.
+ * part_m/part_l: [B, Hq, S, slots] fp32; part_acc [B, Hq, S, slots, D].
+ * Replaces attend_partials (src/moba/kernels/moba_fwd.py:566-665) and
+ * moba_fwd_kernel (moba_fwd.py:230-425).
+ */
+int moba_attend(const void* q, const void* k, const void* v,
+                const int32_t* col_nnz, const int32_t* col_offsets,
+                const int32_t* row_indices, const int32_t* head_indices,
+                const int32_t* slot_of_pair, const int32_t* order,
+                float* part_m, float* part_l, void* part_acc,
+                const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+                int64_t max_seqlen, int64_t h_q, int64_t h_kv,
+                int64_t head_dim, int64_t n_blocks, int64_t block_size,
+                int64_t slots, int64_t index_cap, int causal, int dtype,
+                int acc_dtype, void* stream);
+
+/*
+ * LSE merge of the per-slot partials: out [B, S, Hq, D] (out_dtype) and,
+ * when lse != NULL, lse [B, Hq, S] fp32 in log2 units. Slots with
+ * part_m = -inf are skipped even if their l / acc hold NaN.
+ * Replaces combine_partials (src/moba/kernels/moba_fwd.py:668-725) and
+ * moba_combine_kernel (moba_fwd.py:429-521).
+ */
+int moba_combine(const float* part_m, const float* part_l,
+                 const void* part_acc, void* out, float* lse, int64_t batch,
+                 int64_t seq_len, int64_t h_q, int64_t head_dim,
+                 int64_t slots, int acc_dtype, int out_dtype, void* stream);
+
+/*
+ * delta [B, Hq, S] fp32 = rowsum(dO * O). Replaces compute_delta
+ * (src/moba/kernels/moba_bwd.py:454-470, kernel moba_bwd.py:135-160).
+ */
+int moba_bwd_delta(const void* out, const void* dout, float* delta,
+                   int64_t batch, int64_t seq_len, int64_t h_q,
+                   int64_t head_dim, int dtype, void* stream);
+
+/*
+ * KV-block-major backward: dK, dV [B, S, Hkv, D] (input dtype, every key
+ * written, zero for unselected blocks) and one dQ partial per (query, slot):
+ * dq_part [B, Hq, S, slots, D] (acc_dtype). Replaces the kernel launch in
+ * moba_backward (src/moba/kernels/moba_bwd.py:506-579; kernel
+ * moba_bwd.py:216-394). lse is log2 units as moba_combine writes it.
+ */
+int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
+             const float* lse, const float* delta, const int32_t* col_nnz,
+             const int32_t* col_offsets, const int32_t* row_indices,
+             const int32_t* head_indices, const int32_t* slot_of_pair,
+             const int32_t* order, void* dk, void* dv, void* dq_part,
+             const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+             int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
+             int64_t n_blocks, int64_t block_size, int64_t slots,
+             int64_t index_cap, int causal, int dtype, int acc_dtype,
+             void* stream);
+
+/*
+ * dQ [B, S, Hq, D] = sum over written slots of dq_part, gated by the
+ * forward's part_m written-marker. Replaces reduce_dq
+ * (src/moba/kernels/moba_bwd.py:473-503, kernel moba_bwd.py:398-446).
+ */
+int moba_dq_reduce(const void* dq_part, const float* part_m, void* dq,
+                   int64_t batch, int64_t seq_len, int64_t h_q,
+                   int64_t head_dim, int64_t slots, int acc_dtype,
+                   int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOBA_HIP_H_ */

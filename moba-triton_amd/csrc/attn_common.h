@@ -1,0 +1,82 @@
+// Shared arguments and addressing of the KV-block-major attention kernels.
+#pragma once
+
+#include "common.h"
+
+namespace moba {
+
+// Everything a KV-block-major kernel needs, passed by value.
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* dout;       // backward only
+  const float* lse;       // backward only (log2 units)
+  const float* delta;     // backward only
+  const int32_t* col_nnz;
+  const int32_t* col_offsets;
+  const int32_t* row_indices;
+  const int32_t* head_indices;
+  const int32_t* slot_of_pair;
+  const int32_t* order;
+  const int32_t* cu;
+  float* part_m;          // forward only
+  float* part_l;          // forward only
+  void* part_acc;         // forward: acc partials; backward: dq partials
+  void* dk;               // backward only
+  void* dv;               // backward only
+  int64_t S;              // padded S, or packed token count T
+  int64_t h_q, h_kv, D, n_blocks, bs, slots, cap;
+  int causal;
+  float scale_log2;       // D^-1/2 * log2(e)
+  float scale;            // D^-1/2
+};
+
+// Per-column context resolved from (program column position, row * h_kv).
+struct Column {
+  int64_t r, hk;
+  int64_t blk;
+  int32_t n;       // entries in the column
+  int64_t lo;      // offset of the column in the index arrays (incl. row base)
+  int64_t key0;    // first key position, in the frame row_indices use
+  int64_t key_end; // one past the last valid key position, same frame
+  int64_t tok0;    // global token index of key0 (addresses K / V)
+};
+
+__device__ inline Column resolve_column(const AttnArgs& a, int64_t col_pos, int64_t rh) {
+  Column c;
+  c.r = rh / a.h_kv;
+  c.hk = rh % a.h_kv;
+  c.blk = a.order[rh * a.n_blocks + col_pos];
+  c.n = a.col_nnz[rh * a.n_blocks + c.blk];
+  c.lo = rh * a.cap + a.col_offsets[rh * (a.n_blocks + 1) + c.blk];
+  if (a.cu) {
+    const int64_t bos = a.cu[c.r], eos = a.cu[c.r + 1];
+    c.key0 = bos + c.blk * a.bs;                     // packed: global tokens
+    c.key_end = c.key0 + a.bs < eos ? c.key0 + a.bs : eos;
+    c.tok0 = c.key0;
+  } else {
+    c.key0 = c.blk * a.bs;                           // padded: local positions
+    c.key_end = c.key0 + a.bs < a.S ? c.key0 + a.bs : a.S;
+    c.tok0 = c.r * a.S + c.key0;
+  }
+  return c;
+}
+
+// Token-major element offset of (query row value, head) for this column's row.
+__device__ inline int64_t q_offset(const AttnArgs& a, const Column& c, int32_t row, int32_t head) {
+  const int64_t tok = a.cu ? row : c.r * a.S + row;
+  return (tok * a.h_q + head) * a.D;
+}
+
+// Head-major row of (query, head) in [R * Hq, S] partial / lse buffers.
+__device__ inline int64_t part_row(const AttnArgs& a, const Column& c, int32_t row, int32_t head) {
+  return a.cu ? static_cast<int64_t>(head) * a.S + row : (c.r * a.h_q + head) * a.S + row;
+}
+
+// Kernel launchers implemented per file; each returns MOBA_ERR_UNSUPPORTED
+// when its fast path does not cover the configuration.
+int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hipStream_t st);
+int bwd_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hipStream_t st);
+
+}  // namespace moba

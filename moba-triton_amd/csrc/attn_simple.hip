@@ -1,0 +1,604 @@
+// KV-block-major attention, forward and backward, in plain float32 FMA.
+//
+// This file holds the C ABI entry points of the attention stages and the
+// general kernels behind them: every dtype (the float32 path always runs
+// here), any power-of-two head_dim up to 128 with block_size * head_dim <=
+// 16384. The bf16 / fp16 MFMA kernels (attn_mfma.hip) take the shapes they
+// cover and report MOBA_ERR_UNSUPPORTED otherwise, which routes here.
+//
+// Semantics restated:
+//   attend : src/moba/kernels/moba_fwd.py:230-425 -- per column, queries x
+//            the block's keys, additive tail / causal masks, m = row max of
+//            q.k * D^-1/2 * log2 e, p = exp2(s - m), l = sum p, acc = p V,
+//            stored at the query's fixed slot.
+//   combine: moba_fwd.py:429-521 -- two passes over the slots, skipping slots
+//            whose m is -inf, out = acc / l, lse = m_g + log2 l.
+//   delta  : src/moba/kernels/moba_bwd.py:135-160.
+//   bwd    : moba_bwd.py:216-394 -- p = exp2(s - lse), dv += p^T dO,
+//            ds = p (dO V^T - delta), dk += ds^T Q D^-1/2, dq = ds K D^-1/2.
+//   reduce : moba_bwd.py:398-446 -- sum of written slots.
+//
+// Work per column is split into groups of E entries; everything a group
+// touches is staged in LDS as float32 so each product is formed once.
+#include "attn_common.h"
+
+namespace moba {
+
+constexpr int kE = 16;    // entries per group, forward / dq kernels
+constexpr int kBE = 32;   // entries per group, dk/dv kernel
+constexpr int kKT = 32;   // keys per tile, backward kernels
+
+__device__ inline float neg_inf() { return -INFINITY; }
+
+// ---------------------------------------------------------------------------
+// Forward attend.
+// ---------------------------------------------------------------------------
+template <typename T, typename A>
+__global__ void __launch_bounds__(256)
+attend_simple_kernel(AttnArgs a) {
+  extern __shared__ float smem[];
+  const int64_t D = a.D, bs = a.bs;
+  float* Ks = smem;                 // [bs][D]
+  float* Vs = Ks + bs * D;          // [bs][D]
+  float* Qs = Vs + bs * D;          // [kE][D]
+  float* Ss = Qs + kE * D;          // [kE][bs]
+  float* Ms = Ss + kE * bs;         // [kE]
+  float* Ls = Ms + kE;              // [kE]
+  int* Rs = reinterpret_cast<int*>(Ls + kE);  // rows
+  int* Hs = Rs + kE;                          // heads
+  int* Zs = Hs + kE;                          // slots
+
+  const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
+  if (c.n == 0) return;
+  const T* K = static_cast<const T*>(a.k);
+  const T* V = static_cast<const T*>(a.v);
+  const T* Q = static_cast<const T*>(a.q);
+  for (int64_t i = threadIdx.x; i < bs * D; i += blockDim.x) {
+    const int64_t j = i / D, d = i % D;
+    const bool ok = c.key0 + j < c.key_end;
+    const int64_t off = ((c.tok0 + j) * a.h_kv + c.hk) * D + d;
+    Ks[i] = ok ? Elem<T>::load(K, off) : 0.f;
+    Vs[i] = ok ? Elem<T>::load(V, off) : 0.f;
+  }
+  for (int32_t e0 = 0; e0 < c.n; e0 += kE) {
+    __syncthreads();
+    if (threadIdx.x < kE) {
+      const int32_t e = e0 + threadIdx.x;
+      const bool live = e < c.n;
+      Rs[threadIdx.x] = live ? a.row_indices[c.lo + e] : -1;
+      Hs[threadIdx.x] = live ? a.head_indices[c.lo + e] : 0;
+      Zs[threadIdx.x] = live ? a.slot_of_pair[c.lo + e] : 0;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
+      const int e = static_cast<int>(i / D);
+      const int64_t d = i % D;
+      Qs[i] = Rs[e] >= 0 ? Elem<T>::load(Q, q_offset(a, c, Rs[e], Hs[e]) + d) : 0.f;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < kE * bs; i += blockDim.x) {
+      const int e = static_cast<int>(i / bs);
+      const int64_t j = i % bs;
+      const int64_t kpos = c.key0 + j;
+      float s = 0.f;
+      for (int64_t d = 0; d < D; ++d) s = fmaf(Qs[e * D + d], Ks[j * D + d], s);
+      s *= a.scale_log2;
+      const bool ok = kpos < c.key_end && (!a.causal || kpos <= Rs[e]);
+      Ss[i] = ok ? s : neg_inf();
+    }
+    __syncthreads();
+    if (threadIdx.x < kE) {
+      const int e = threadIdx.x;
+      float m = neg_inf();
+      for (int64_t j = 0; j < bs; ++j) m = fmaxf(m, Ss[e * bs + j]);
+      float l = 0.f;
+      for (int64_t j = 0; j < bs; ++j) {
+        const float p = Ss[e * bs + j] > neg_inf() ? exp2f(Ss[e * bs + j] - m) : 0.f;
+        Ss[e * bs + j] = p;
+        l += p;
+      }
+      Ms[e] = m;
+      Ls[e] = l;
+      if (Rs[e] >= 0) {
+        const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
+        a.part_m[dst] = m;
+        a.part_l[dst] = l;
+      }
+    }
+    __syncthreads();
+    A* acc_out = static_cast<A*>(a.part_acc);
+    for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
+      const int e = static_cast<int>(i / D);
+      const int64_t d = i % D;
+      if (Rs[e] < 0) continue;
+      float acc = 0.f;
+      for (int64_t j = 0; j < bs; ++j) acc = fmaf(Ss[e * bs + j], Vs[j * D + d], acc);
+      const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
+      Elem<A>::store(acc_out, dst * D + d, acc);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: dK / dV per key tile, one program per (column, key tile).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256)
+bwd_dkdv_simple_kernel(AttnArgs a) {
+  extern __shared__ float smem[];
+  const int64_t D = a.D;
+  float* Kt = smem;                 // [kKT][D]
+  float* Vt = Kt + kKT * D;         // [kKT][D]
+  float* Qs = Vt + kKT * D;         // [kBE][D]
+  float* Os = Qs + kBE * D;         // [kBE][D]  (dO)
+  float* Ps = Os + kBE * D;         // [kBE][kKT]
+  float* Gs = Ps + kBE * kKT;       // [kBE][kKT] (dS)
+  float* Lse = Gs + kBE * kKT;      // [kBE]
+  float* Dl = Lse + kBE;            // [kBE]
+  int* Rs = reinterpret_cast<int*>(Dl + kBE);
+  int* Hs = Rs + kBE;
+
+  const int64_t tiles = (a.bs + kKT - 1) / kKT;
+  const Column c = resolve_column(a, blockIdx.x / tiles, blockIdx.y);
+  const int64_t kt0 = (blockIdx.x % tiles) * kKT;
+  const T* K = static_cast<const T*>(a.k);
+  const T* V = static_cast<const T*>(a.v);
+  const T* Q = static_cast<const T*>(a.q);
+  const T* dO = static_cast<const T*>(a.dout);
+  for (int64_t i = threadIdx.x; i < kKT * D; i += blockDim.x) {
+    const int64_t j = i / D, d = i % D;
+    const bool ok = kt0 + j < a.bs && c.key0 + kt0 + j < c.key_end;
+    const int64_t off = ((c.tok0 + kt0 + j) * a.h_kv + c.hk) * D + d;
+    Kt[i] = ok ? Elem<T>::load(K, off) : 0.f;
+    Vt[i] = ok ? Elem<T>::load(V, off) : 0.f;
+  }
+  // Accumulators for the (key, feature) elements this thread owns.
+  constexpr int kMaxOwn = (kKT * 128) / 256;
+  float dk[kMaxOwn], dv[kMaxOwn];
+#pragma unroll
+  for (int u = 0; u < kMaxOwn; ++u) { dk[u] = 0.f; dv[u] = 0.f; }
+  const int own = static_cast<int>((kKT * D) / 256);
+  for (int32_t e0 = 0; e0 < c.n; e0 += kBE) {
+    __syncthreads();
+    if (threadIdx.x < kBE) {
+      const int32_t e = e0 + threadIdx.x;
+      const bool live = e < c.n;
+      const int32_t row = live ? a.row_indices[c.lo + e] : -1;
+      const int32_t head = live ? a.head_indices[c.lo + e] : 0;
+      Rs[threadIdx.x] = row;
+      Hs[threadIdx.x] = head;
+      Lse[threadIdx.x] = live ? a.lse[part_row(a, c, row, head)] : 0.f;
+      Dl[threadIdx.x] = live ? a.delta[part_row(a, c, row, head)] : 0.f;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < kBE * D; i += blockDim.x) {
+      const int e = static_cast<int>(i / D);
+      const int64_t d = i % D;
+      const bool live = Rs[e] >= 0;
+      const int64_t off = live ? q_offset(a, c, Rs[e], Hs[e]) + d : 0;
+      Qs[i] = live ? Elem<T>::load(Q, off) : 0.f;
+      Os[i] = live ? Elem<T>::load(dO, off) : 0.f;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < kBE * kKT; i += blockDim.x) {
+      const int e = static_cast<int>(i / kKT);
+      const int64_t j = i % kKT;
+      const int64_t kpos = c.key0 + kt0 + j;
+      float s = 0.f, dp = 0.f;
+      for (int64_t d = 0; d < D; ++d) {
+        s = fmaf(Qs[e * D + d], Kt[j * D + d], s);
+        dp = fmaf(Os[e * D + d], Vt[j * D + d], dp);
+      }
+      const bool ok = Rs[e] >= 0 && kt0 + j < a.bs && kpos < c.key_end &&
+                      (!a.causal || kpos <= Rs[e]);
+      const float p = ok ? exp2f(s * a.scale_log2 - Lse[e]) : 0.f;
+      Ps[i] = p;
+      Gs[i] = p * (dp - Dl[e]);
+    }
+    __syncthreads();
+    for (int u = 0; u < own; ++u) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(u) * blockDim.x;
+      const int64_t j = i / D, d = i % D;
+      float adk = dk[u], adv = dv[u];
+      for (int e = 0; e < kBE; ++e) {
+        adv = fmaf(Ps[e * kKT + j], Os[e * D + d], adv);
+        adk = fmaf(Gs[e * kKT + j], Qs[e * D + d], adk);
+      }
+      dk[u] = adk;
+      dv[u] = adv;
+    }
+  }
+  T* dK = static_cast<T*>(a.dk);
+  T* dV = static_cast<T*>(a.dv);
+  for (int u = 0; u < own; ++u) {
+    const int64_t i = threadIdx.x + static_cast<int64_t>(u) * blockDim.x;
+    const int64_t j = i / D, d = i % D;
+    if (kt0 + j >= a.bs || c.key0 + kt0 + j >= c.key_end) continue;
+    const int64_t off = ((c.tok0 + kt0 + j) * a.h_kv + c.hk) * D + d;
+    Elem<T>::store(dK, off, dk[u] * a.scale);
+    Elem<T>::store(dV, off, dv[u]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: per-slot dQ partials, one program per column.
+// ---------------------------------------------------------------------------
+template <typename T, typename A>
+__global__ void __launch_bounds__(256)
+bwd_dq_simple_kernel(AttnArgs a) {
+  extern __shared__ float smem[];
+  const int64_t D = a.D;
+  float* Kt = smem;                 // [kKT][D]
+  float* Vt = Kt + kKT * D;         // [kKT][D]
+  float* Qs = Vt + kKT * D;         // [kE][D]
+  float* Os = Qs + kE * D;          // [kE][D]
+  float* Gs = Os + kE * D;          // [kE][kKT]
+  float* Lse = Gs + kE * kKT;       // [kE]
+  float* Dl = Lse + kE;             // [kE]
+  int* Rs = reinterpret_cast<int*>(Dl + kE);
+  int* Hs = Rs + kE;
+  int* Zs = Hs + kE;
+
+  const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
+  if (c.n == 0) return;
+  const T* K = static_cast<const T*>(a.k);
+  const T* V = static_cast<const T*>(a.v);
+  const T* Q = static_cast<const T*>(a.q);
+  const T* dO = static_cast<const T*>(a.dout);
+  A* out = static_cast<A*>(a.part_acc);
+  constexpr int kMaxOwn = (kE * 128) / 256;
+  const int own = static_cast<int>((kE * D) / 256);
+  for (int32_t e0 = 0; e0 < c.n; e0 += kE) {
+    __syncthreads();
+    if (threadIdx.x < kE) {
+      const int32_t e = e0 + threadIdx.x;
+      const bool live = e < c.n;
+      const int32_t row = live ? a.row_indices[c.lo + e] : -1;
+      const int32_t head = live ? a.head_indices[c.lo + e] : 0;
+      Rs[threadIdx.x] = row;
+      Hs[threadIdx.x] = head;
+      Zs[threadIdx.x] = live ? a.slot_of_pair[c.lo + e] : 0;
+      Lse[threadIdx.x] = live ? a.lse[part_row(a, c, row, head)] : 0.f;
+      Dl[threadIdx.x] = live ? a.delta[part_row(a, c, row, head)] : 0.f;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
+      const int e = static_cast<int>(i / D);
+      const int64_t d = i % D;
+      const bool live = Rs[e] >= 0;
+      const int64_t off = live ? q_offset(a, c, Rs[e], Hs[e]) + d : 0;
+      Qs[i] = live ? Elem<T>::load(Q, off) : 0.f;
+      Os[i] = live ? Elem<T>::load(dO, off) : 0.f;
+    }
+    float dq[kMaxOwn];
+#pragma unroll
+    for (int u = 0; u < kMaxOwn; ++u) dq[u] = 0.f;
+    for (int64_t kt0 = 0; kt0 < a.bs; kt0 += kKT) {
+      __syncthreads();
+      for (int64_t i = threadIdx.x; i < kKT * D; i += blockDim.x) {
+        const int64_t j = i / D, d = i % D;
+        const bool ok = kt0 + j < a.bs && c.key0 + kt0 + j < c.key_end;
+        const int64_t off = ((c.tok0 + kt0 + j) * a.h_kv + c.hk) * D + d;
+        Kt[i] = ok ? Elem<T>::load(K, off) : 0.f;
+        Vt[i] = ok ? Elem<T>::load(V, off) : 0.f;
+      }
+      __syncthreads();
+      for (int64_t i = threadIdx.x; i < kE * kKT; i += blockDim.x) {
+        const int e = static_cast<int>(i / kKT);
+        const int64_t j = i % kKT;
+        const int64_t kpos = c.key0 + kt0 + j;
+        float s = 0.f, dp = 0.f;
+        for (int64_t d = 0; d < D; ++d) {
+          s = fmaf(Qs[e * D + d], Kt[j * D + d], s);
+          dp = fmaf(Os[e * D + d], Vt[j * D + d], dp);
+        }
+        const bool ok = Rs[e] >= 0 && kt0 + j < a.bs && kpos < c.key_end &&
+                        (!a.causal || kpos <= Rs[e]);
+        const float p = ok ? exp2f(s * a.scale_log2 - Lse[e]) : 0.f;
+        Gs[i] = p * (dp - Dl[e]);
+      }
+      __syncthreads();
+      for (int u = 0; u < own; ++u) {
+        const int64_t i = threadIdx.x + static_cast<int64_t>(u) * blockDim.x;
+        const int e = static_cast<int>(i / D);
+        const int64_t d = i % D;
+        float acc = dq[u];
+        for (int64_t j = 0; j < kKT; ++j) acc = fmaf(Gs[e * kKT + j], Kt[j * D + d], acc);
+        dq[u] = acc;
+      }
+    }
+    for (int u = 0; u < own; ++u) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(u) * blockDim.x;
+      const int e = static_cast<int>(i / D);
+      const int64_t d = i % D;
+      if (Rs[e] < 0) continue;
+      const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
+      Elem<A>::store(out, dst * D + d, dq[u] * a.scale);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row-wise passes: combine, delta, dq reduce.
+// ---------------------------------------------------------------------------
+template <typename A, typename O>
+__global__ void __launch_bounds__(256)
+combine_kernel(const float* __restrict__ part_m, const float* __restrict__ part_l,
+               const A* __restrict__ part_acc, O* __restrict__ out, float* __restrict__ lse,
+               int64_t n_rows, int64_t S, int64_t h_q, int64_t D, int64_t slots) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gid / D;     // head-major (b * Hq + h) * S + t
+  const int64_t d = gid % D;
+  if (row >= n_rows) return;
+  const float* m = part_m + row * slots;
+  const float* l = part_l + row * slots;
+  float m_g = -INFINITY;
+  for (int64_t j = 0; j < slots; ++j) m_g = fmaxf(m_g, m[j]);
+  float ls = 0.f, acc = 0.f;
+  for (int64_t j = 0; j < slots; ++j) {
+    const float mi = m[j];
+    if (mi > -INFINITY) {
+      const float w = exp2f(mi - m_g);
+      ls += l[j] * w;
+      acc += Elem<A>::load(part_acc, (row * slots + j) * D + d) * w;
+    }
+  }
+  const int64_t bh = row / S, t = row % S;
+  const int64_t b = bh / h_q, h = bh % h_q;
+  Elem<O>::store(out, ((b * S + t) * h_q + h) * D + d, acc / ls);
+  if (lse && d == 0) lse[row] = m_g + log2f(ls);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, float* __restrict__ delta,
+             int64_t n_rows, int64_t S, int64_t h_q, int64_t D) {
+  // One wave per query row; lanes stride the features.
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
+  const int lane = threadIdx.x & 63;
+  if (row >= n_rows) return;
+  const int64_t bh = row / S, t = row % S;
+  const int64_t b = bh / h_q, h = bh % h_q;
+  const int64_t base = ((b * S + t) * h_q + h) * D;
+  float acc = 0.f;
+  for (int64_t d = lane; d < D; d += 64)
+    acc = fmaf(Elem<T>::load(o, base + d), Elem<T>::load(dout, base + d), acc);
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (lane == 0) delta[row] = acc;
+}
+
+template <typename A, typename O>
+__global__ void __launch_bounds__(256)
+dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m,
+                 O* __restrict__ dq, int64_t n_rows, int64_t S, int64_t h_q, int64_t D,
+                 int64_t slots) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gid / D;
+  const int64_t d = gid % D;
+  if (row >= n_rows) return;
+  float acc = 0.f;
+  for (int64_t j = 0; j < slots; ++j)
+    if (part_m[row * slots + j] > -INFINITY)
+      acc += Elem<A>::load(dq_part, (row * slots + j) * D + d);
+  const int64_t bh = row / S, t = row % S;
+  const int64_t b = bh / h_q, h = bh % h_q;
+  Elem<O>::store(dq, ((b * S + t) * h_q + h) * D + d, acc);
+}
+
+__global__ void __launch_bounds__(256)
+fill_f32_kernel(float* __restrict__ p, int64_t n, float value) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = value;
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+static int prepare_attn(AttnArgs* a, Geometry* g, const void* q, const void* k,
+                        const void* v, const int32_t* col_nnz, const int32_t* col_offsets,
+                        const int32_t* row_indices, const int32_t* head_indices,
+                        const int32_t* slot_of_pair, const int32_t* order,
+                        const int32_t* cu, int64_t batch, int64_t seq_len,
+                        int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
+                        int64_t n_blocks, int64_t block_size, int64_t slots,
+                        int64_t index_cap, int causal) {
+  int st = make_geometry(g, batch, seq_len, max_seqlen, h_q, h_kv, head_dim, n_blocks,
+                         block_size, slots, cu);
+  if (st) return st;
+  if (!q || !k || !v || !col_nnz || !col_offsets || !row_indices || !head_indices ||
+      !slot_of_pair || !order)
+    return fail(MOBA_ERR_INVALID, "null pointer");
+  if (slots <= 0) return fail(MOBA_ERR_INVALID, "slots must be positive");
+  if (index_cap < g->group * g->rows_per_seq * slots)
+    return fail(MOBA_ERR_INVALID, "index capacity below group * rows * slots");
+  if (head_dim & (head_dim - 1))
+    return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a power of two");
+  *a = AttnArgs{};
+  a->q = q; a->k = k; a->v = v;
+  a->col_nnz = col_nnz; a->col_offsets = col_offsets; a->row_indices = row_indices;
+  a->head_indices = head_indices; a->slot_of_pair = slot_of_pair; a->order = order;
+  a->cu = cu;
+  a->S = seq_len; a->h_q = h_q; a->h_kv = h_kv; a->D = head_dim; a->n_blocks = n_blocks;
+  a->bs = block_size; a->slots = slots; a->cap = index_cap; a->causal = causal ? 1 : 0;
+  a->scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+  a->scale_log2 = a->scale * 1.4426950408889634f;
+  return MOBA_OK;
+}
+
+static bool simple_shape_ok(const Geometry& g) {
+  return g.head_dim <= 128 && g.head_dim >= 8 && g.block_size * g.head_dim <= 16384;
+}
+
+template <typename K>
+static int set_lds(K kernel, size_t bytes) {
+  if (bytes > 160 * 1024) return fail(MOBA_ERR_UNSUPPORTED, "tile exceeds LDS");
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(bytes));
+  if (e != hipSuccess) return fail(MOBA_ERR_LAUNCH, hipGetErrorString(e));
+  return MOBA_OK;
+}
+
+#define MOBA_DISPATCH_ACC(code, A, ...)                                   \
+  [&]() -> int {                                                          \
+    switch (code) {                                                       \
+      case MOBA_BF16: { using A = ::moba::bf16_t; return __VA_ARGS__(); } \
+      case MOBA_FP16: { using A = ::moba::f16_t; return __VA_ARGS__(); }  \
+      case MOBA_FP32: { using A = float; return __VA_ARGS__(); }          \
+      default:                                                            \
+        return ::moba::fail(MOBA_ERR_UNSUPPORTED, "unknown dtype code");  \
+    }                                                                     \
+  }()
+
+}  // namespace moba
+
+extern "C" int moba_attend(const void* q, const void* k, const void* v,
+                           const int32_t* col_nnz, const int32_t* col_offsets,
+                           const int32_t* row_indices, const int32_t* head_indices,
+                           const int32_t* slot_of_pair, const int32_t* order,
+                           float* part_m, float* part_l, void* part_acc,
+                           const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+                           int64_t max_seqlen, int64_t h_q, int64_t h_kv,
+                           int64_t head_dim, int64_t n_blocks, int64_t block_size,
+                           int64_t slots, int64_t index_cap, int causal, int dtype,
+                           int acc_dtype, void* stream) {
+  using namespace moba;
+  AttnArgs a;
+  Geometry g;
+  int st = prepare_attn(&a, &g, q, k, v, col_nnz, col_offsets, row_indices, head_indices,
+                        slot_of_pair, order, cu_seqlens, batch, seq_len, max_seqlen, h_q,
+                        h_kv, head_dim, n_blocks, block_size, slots, index_cap, causal);
+  if (st) return st;
+  if (!part_m || !part_l || !part_acc) return fail(MOBA_ERR_INVALID, "null partials");
+  a.part_m = part_m; a.part_l = part_l; a.part_acc = part_acc;
+  hipStream_t s = as_stream(stream);
+  // Unwritten slots must read as m = -inf: the marker combine and dq reduce
+  // rely on. Only part_m is cleared; l / acc of such slots are never read.
+  const int64_t n_m = (g.packed ? 1 : batch) * h_q * seq_len * slots;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(static_cast<unsigned>(cdiv(n_m, 256) < 8192 ? cdiv(n_m, 256) : 8192)),
+                     dim3(256), 0, s, part_m, n_m, -INFINITY);
+  st = check_launch("moba_attend (fill)");
+  if (st) return st;
+  st = attend_mfma(a, dtype, acc_dtype, batch * h_kv, s);
+  if (st != MOBA_ERR_UNSUPPORTED) return st;
+  if (!simple_shape_ok(g))
+    return fail(MOBA_ERR_UNSUPPORTED, "attend: block_size * head_dim must be <= 16384");
+  const size_t lds = sizeof(float) * (2 * block_size * head_dim + kE * head_dim +
+                                      kE * block_size + 2 * kE) + sizeof(int) * 3 * kE;
+  dim3 grid(static_cast<unsigned>(n_blocks), static_cast<unsigned>(batch * h_kv));
+  return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
+    return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
+      int rc = set_lds(attend_simple_kernel<T, A>, lds);
+      if (rc) return rc;
+      hipLaunchKernelGGL((attend_simple_kernel<T, A>), grid, dim3(256), lds, s, a);
+      return check_launch("moba_attend");
+    });
+  });
+}
+
+extern "C" int moba_combine(const float* part_m, const float* part_l, const void* part_acc,
+                            void* out, float* lse, int64_t batch, int64_t seq_len,
+                            int64_t h_q, int64_t head_dim, int64_t slots, int acc_dtype,
+                            int out_dtype, void* stream) {
+  using namespace moba;
+  if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0 || slots <= 0)
+    return fail(MOBA_ERR_INVALID, "non-positive shape argument");
+  if (!part_m || !part_l || !part_acc || !out) return fail(MOBA_ERR_INVALID, "null pointer");
+  const int64_t n_rows = batch * h_q * seq_len;
+  dim3 grid(static_cast<unsigned>(cdiv(n_rows * head_dim, 256)));
+  return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
+    return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
+      hipLaunchKernelGGL((combine_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
+                         part_m, part_l, static_cast<const A*>(part_acc), static_cast<O*>(out),
+                         lse, n_rows, seq_len, h_q, head_dim, slots);
+      return check_launch("moba_combine");
+    });
+  });
+}
+
+extern "C" int moba_bwd_delta(const void* out, const void* dout, float* delta, int64_t batch,
+                              int64_t seq_len, int64_t h_q, int64_t head_dim, int dtype,
+                              void* stream) {
+  using namespace moba;
+  if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0)
+    return fail(MOBA_ERR_INVALID, "non-positive shape argument");
+  if (!out || !dout || !delta) return fail(MOBA_ERR_INVALID, "null pointer");
+  const int64_t n_rows = batch * h_q * seq_len;
+  dim3 grid(static_cast<unsigned>(cdiv(n_rows * 64, 256)));
+  return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
+    hipLaunchKernelGGL(delta_kernel<T>, grid, dim3(256), 0, as_stream(stream),
+                       static_cast<const T*>(out), static_cast<const T*>(dout), delta, n_rows,
+                       seq_len, h_q, head_dim);
+    return check_launch("moba_bwd_delta");
+  });
+}
+
+extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
+                        const float* lse, const float* delta, const int32_t* col_nnz,
+                        const int32_t* col_offsets, const int32_t* row_indices,
+                        const int32_t* head_indices, const int32_t* slot_of_pair,
+                        const int32_t* order, void* dk, void* dv, void* dq_part,
+                        const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+                        int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
+                        int64_t n_blocks, int64_t block_size, int64_t slots,
+                        int64_t index_cap, int causal, int dtype, int acc_dtype,
+                        void* stream) {
+  using namespace moba;
+  AttnArgs a;
+  Geometry g;
+  int st = prepare_attn(&a, &g, q, k, v, col_nnz, col_offsets, row_indices, head_indices,
+                        slot_of_pair, order, cu_seqlens, batch, seq_len, max_seqlen, h_q,
+                        h_kv, head_dim, n_blocks, block_size, slots, index_cap, causal);
+  if (st) return st;
+  if (!dout || !lse || !delta || !dk || !dv || !dq_part)
+    return fail(MOBA_ERR_INVALID, "null pointer");
+  a.dout = dout; a.lse = lse; a.delta = delta; a.dk = dk; a.dv = dv; a.part_acc = dq_part;
+  hipStream_t s = as_stream(stream);
+  st = bwd_mfma(a, dtype, acc_dtype, batch * h_kv, s);
+  if (st != MOBA_ERR_UNSUPPORTED) return st;
+  if (head_dim > 128 || head_dim < 8)
+    return fail(MOBA_ERR_UNSUPPORTED, "backward: head_dim must be in [8, 128]");
+  const int64_t tiles = cdiv(block_size, kKT);
+  const size_t lds_kv = sizeof(float) * (2 * kKT * head_dim + 2 * kBE * head_dim +
+                                         2 * kBE * kKT + 2 * kBE) + sizeof(int) * 2 * kBE;
+  const size_t lds_q = sizeof(float) * (2 * kKT * head_dim + 2 * kE * head_dim +
+                                        kE * kKT + 2 * kE) + sizeof(int) * 3 * kE;
+  return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
+    return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
+      int rc = set_lds(bwd_dkdv_simple_kernel<T>, lds_kv);
+      if (rc) return rc;
+      rc = set_lds(bwd_dq_simple_kernel<T, A>, lds_q);
+      if (rc) return rc;
+      hipLaunchKernelGGL(bwd_dkdv_simple_kernel<T>,
+                         dim3(static_cast<unsigned>(n_blocks * tiles),
+                              static_cast<unsigned>(batch * h_kv)),
+                         dim3(256), lds_kv, s, a);
+      rc = check_launch("moba_bwd (dk/dv)");
+      if (rc) return rc;
+      hipLaunchKernelGGL((bwd_dq_simple_kernel<T, A>),
+                         dim3(static_cast<unsigned>(n_blocks), static_cast<unsigned>(batch * h_kv)),
+                         dim3(256), lds_q, s, a);
+      return check_launch("moba_bwd (dq)");
+    });
+  });
+}
+
+extern "C" int moba_dq_reduce(const void* dq_part, const float* part_m, void* dq,
+                              int64_t batch, int64_t seq_len, int64_t h_q, int64_t head_dim,
+                              int64_t slots, int acc_dtype, int out_dtype, void* stream) {
+  using namespace moba;
+  if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0 || slots <= 0)
+    return fail(MOBA_ERR_INVALID, "non-positive shape argument");
+  if (!dq_part || !part_m || !dq) return fail(MOBA_ERR_INVALID, "null pointer");
+  const int64_t n_rows = batch * h_q * seq_len;
+  dim3 grid(static_cast<unsigned>(cdiv(n_rows * head_dim, 256)));
+  return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
+    return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
+      hipLaunchKernelGGL((dq_reduce_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
+                         static_cast<const A*>(dq_part), part_m, static_cast<O*>(dq), n_rows,
+                         seq_len, h_q, head_dim, slots);
+      return check_launch("moba_dq_reduce");
+    });
+  });
+}

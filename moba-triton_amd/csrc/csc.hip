@@ -1,0 +1,168 @@
+// CSC transpose of the gate's per-query block ids into per-block columns.
+//
+// Restates src/moba/kernels/routing.py:139-301 (count / offsets+order /
+// scatter) and routing.py:309-427 (launcher): counts per (row, kv head,
+// block) with atomics, an exclusive scan into col_offsets, a longest-first
+// column order (count desc, id asc; the stable argsort of routing.py:548-553),
+// and an atomic-cursor scatter of (row, query head, slot) triples. Under GQA
+// every query head of a group lands in its kv head's columns.
+//
+// The order pass ranks each column directly -- rank = #columns with a larger
+// count, or the same count and a smaller id -- one lane per column against an
+// LDS copy of the counts. It is O(nb^2) work spread over nb lanes; at
+// nb = 4096 that is ~16M integer compares per head, a few microseconds.
+#include "common.h"
+
+namespace moba {
+
+__global__ void __launch_bounds__(256)
+fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t value) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = value;
+}
+
+// One lane per (query, slot) entry; grid.y = row * Hq + hq.
+template <bool kScatter>
+__global__ void __launch_bounds__(256)
+count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restrict__ cu,
+                        int64_t S, int64_t rows_per_seq, int64_t h_q, int64_t h_kv,
+                        int64_t n_blocks, int slots, int64_t cap,
+                        int32_t* __restrict__ col_nnz_or_cursor,
+                        const int32_t* __restrict__ col_offsets,
+                        int32_t* __restrict__ row_indices, int32_t* __restrict__ head_indices,
+                        int32_t* __restrict__ slot_of_pair) {
+  const int64_t rh = blockIdx.y;
+  const int64_t r = rh / h_q;
+  const int64_t hq = rh % h_q;
+  const int64_t hk = hq / (h_q / h_kv);
+  const bool packed = cu != nullptr;
+  const SeqSpan sp = seq_span(cu, r, S);
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t t = e / slots;
+  const int j = static_cast<int>(e % slots);
+  if (t >= sp.len) return;
+  const int64_t tok = sp.bos + t;
+  const int64_t qid = packed ? hq * S + tok : (r * h_q + hq) * S + t;
+  const int32_t blk = block_idx[qid * slots + j];
+  if (blk < 0) return;
+  const int64_t colbase = (r * h_kv + hk) * n_blocks;
+  const int32_t within = atomicAdd(&col_nnz_or_cursor[colbase + blk], 1);
+  if (kScatter) {
+    const int64_t dst = (r * h_kv + hk) * cap +
+                        col_offsets[(r * h_kv + hk) * (n_blocks + 1) + blk] + within;
+    row_indices[dst] = static_cast<int32_t>(packed ? tok : t);
+    head_indices[dst] = static_cast<int32_t>(hq);
+    slot_of_pair[dst] = j;
+  }
+}
+
+// Exclusive scan of one (row, kv head)'s counts; one workgroup each.
+__global__ void __launch_bounds__(1024)
+scan_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ col_offsets,
+            int64_t n_blocks) {
+  __shared__ int32_t buf[1024];
+  const int64_t rh = blockIdx.x;
+  const int32_t* cnt = col_nnz + rh * n_blocks;
+  int32_t* off = col_offsets + rh * (n_blocks + 1);
+  int32_t carry = 0;
+  for (int64_t base = 0; base < n_blocks; base += 1024) {
+    const int64_t i = base + threadIdx.x;
+    const int32_t x = i < n_blocks ? cnt[i] : 0;
+    buf[threadIdx.x] = x;
+    __syncthreads();
+    for (int s = 1; s < 1024; s <<= 1) {
+      int32_t y = threadIdx.x >= s ? buf[threadIdx.x - s] : 0;
+      __syncthreads();
+      buf[threadIdx.x] += y;
+      __syncthreads();
+    }
+    if (i < n_blocks) off[i] = carry + buf[threadIdx.x] - x;
+    const int32_t total = buf[1023];
+    __syncthreads();
+    carry += total;
+  }
+  if (threadIdx.x == 0) off[n_blocks] = carry;
+}
+
+// order[rank(c)] = c with rank by (count desc, id asc).
+__global__ void __launch_bounds__(256)
+order_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ order,
+             int64_t n_blocks) {
+  __shared__ int32_t tile[4096];
+  const int64_t rh = blockIdx.y;
+  const int32_t* cnt = col_nnz + rh * n_blocks;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int32_t mine = c < n_blocks ? cnt[c] : 0;
+  int64_t rank = 0;
+  for (int64_t base = 0; base < n_blocks; base += 4096) {
+    const int64_t len = n_blocks - base < 4096 ? n_blocks - base : 4096;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) tile[i] = cnt[base + i];
+    __syncthreads();
+    if (c < n_blocks) {
+      for (int64_t i = 0; i < len; ++i) {
+        const int32_t o = tile[i];
+        const int64_t id = base + i;
+        rank += (o > mine || (o == mine && id < c)) ? 1 : 0;
+      }
+    }
+  }
+  if (c < n_blocks) order[rh * n_blocks + rank] = static_cast<int32_t>(c);
+}
+
+}  // namespace moba
+
+extern "C" size_t moba_csc_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q,
+                                          int64_t h_kv, int64_t n_blocks, int64_t slots) {
+  (void)seq_len; (void)h_q; (void)slots;
+  return sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n_blocks);
+}
+
+extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
+                              int32_t* col_offsets, int32_t* row_indices,
+                              int32_t* head_indices, int32_t* slot_of_pair,
+                              int32_t* order, const int32_t* cu_seqlens, int64_t batch,
+                              int64_t seq_len, int64_t max_seqlen, int64_t h_q,
+                              int64_t h_kv, int64_t n_blocks, int64_t slots,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace moba;
+  Geometry g;
+  const int64_t rps = cu_seqlens ? max_seqlen : seq_len;
+  int st = make_geometry(&g, batch, seq_len, max_seqlen, h_q, h_kv, 64, n_blocks,
+                         n_blocks > 0 ? cdiv(rps, n_blocks) : 1, slots, cu_seqlens);
+  if (st) return st;
+  if (slots <= 0) return fail(MOBA_ERR_INVALID, "slots must be positive");
+  if (!block_idx || !col_nnz || !col_offsets || !row_indices || !head_indices ||
+      !slot_of_pair || !order)
+    return fail(MOBA_ERR_INVALID, "null pointer");
+  const size_t need = moba_csc_workspace_size(batch, seq_len, h_q, h_kv, n_blocks, slots);
+  if (!workspace || workspace_bytes < need)
+    return fail(MOBA_ERR_WORKSPACE, "csc workspace too small");
+  const int64_t cap = g.group * g.rows_per_seq * slots;
+  if (cap >= (int64_t(1) << 31))
+    return fail(MOBA_ERR_UNSUPPORTED, "column capacity exceeds int32 offsets");
+  hipStream_t s = as_stream(stream);
+  int32_t* cursor = static_cast<int32_t*>(workspace);
+  const int64_t ncols = batch * h_kv * n_blocks;
+  const unsigned fill_blocks = static_cast<unsigned>(cdiv(ncols, 256) < 4096 ? cdiv(ncols, 256) : 4096);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, col_nnz, ncols, 0);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, cursor, ncols, 0);
+  dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq * slots, 256)),
+            static_cast<unsigned>(batch * h_q));
+  hipLaunchKernelGGL(count_or_scatter_kernel<false>, grid, dim3(256), 0, s, block_idx,
+                     cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
+                     static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
+                     nullptr);
+  hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024), 0, s,
+                     col_nnz, col_offsets, n_blocks);
+  hipLaunchKernelGGL(order_kernel,
+                     dim3(static_cast<unsigned>(cdiv(n_blocks, 256)),
+                          static_cast<unsigned>(batch * h_kv)),
+                     dim3(256), 0, s, col_nnz, order, n_blocks);
+  hipLaunchKernelGGL(count_or_scatter_kernel<true>, grid, dim3(256), 0, s, block_idx,
+                     cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
+                     static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
+                     head_indices, slot_of_pair);
+  return check_launch("moba_csc_build");
+}

@@ -1,0 +1,556 @@
+// MoBA gate: per query, the top `take` strictly-past blocks by q . kbar.
+//
+// Semantics: src/moba/naive.py:64-146 (ranking by score desc, block id asc,
+// i.e. the stable descending argsort of naive.py:124-127; -inf leftovers
+// dropped; own block forced when always_current), emitted ascending with -1
+// padding as src/moba/kernels/gating.py:300-335 does. The score is the exact
+// dot product rounded once to float32 and once to the input dtype.
+//
+// Two kernels:
+//
+// * gate_mfma_kernel (bf16 / fp16, the product path). Each wave owns 32
+//   queries of one (row, query head). Block representatives stream past in
+//   chunks of 32; v_mfma_f32_32x32x16 computes an approximate float32 score
+//   tile S^T[block][query] with the query on the lane axis, so every lane
+//   holds 16 scores of one query and the top-k bookkeeping never crosses
+//   lanes. Scores above the lane's running threshold are appended to a
+//   per-lane LDS buffer; when a buffer fills, it is folded into a sorted
+//   register list of the M best approximate scores and the threshold rises
+//   to the M-th best. At the end the two lanes sharing a query merge their
+//   lists, and only candidates within the provable error band of the T-th
+//   best are rescored exactly (float64, sequential, same as the oracle).
+//   The error band: any float32 summation of D bf16 products is within
+//   D * 2^-24 * sum|q_d kbar_d| <= D * 2^-24 * |q| |kbar| of the exact dot;
+//   the kernel uses 2^-14 |q| max|kbar| (>= 16x that bound at D <= 128) and
+//   a 2^-6 relative gap so two values separated by more than the band can
+//   never round to the same bf16/fp16 score. A query whose evidence is
+//   insufficient (near-ties beyond the list capacity, e.g. constructed
+//   ties) is queued for the exact kernel; it is never guessed.
+//
+// * gate_exact_kernel (fp32, and the queue above). One thread per query,
+//   exact float64 scores for every candidate, streaming top-T in registers.
+#include "common.h"
+
+namespace moba {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+// Workspace layout (bytes): [0, 256) counter; [256, 256 + 4*R*Hkv) norms
+// rounded up to 256; then the queue of query ids (int64 each).
+struct GateWs {
+  int* counter;
+  float* kbar_norm;
+  int64_t* queue;
+  int64_t queue_cap;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+static GateWs gate_ws(void* base, int64_t rows, int64_t h_kv, int64_t queue_cap) {
+  char* p = static_cast<char*>(base);
+  GateWs w;
+  w.counter = reinterpret_cast<int*>(p);
+  w.kbar_norm = reinterpret_cast<float*>(p + 256);
+  w.queue = reinterpret_cast<int64_t*>(p + 256 + align256(sizeof(float) * rows * h_kv));
+  w.queue_cap = queue_cap;
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// Prologue: max |kbar_j| per (row, kv head); clears the queue counter.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256)
+gate_prep_kernel(const T* __restrict__ kbar, const int32_t* __restrict__ cu,
+                 int64_t S, int64_t h_kv, int64_t n_blocks, int64_t D, int64_t bs,
+                 float* __restrict__ norm_out, int* __restrict__ counter) {
+  const int64_t rh = blockIdx.x;
+  if (rh == 0 && threadIdx.x == 0) *counter = 0;
+  // Only the blocks a sequence owns hold data; the tail of a packed kbar row
+  // is never read by the gate and may be uninitialised.
+  const SeqSpan sp = seq_span(cu, rh / h_kv, S);
+  const int64_t owned = (sp.len + bs - 1) / bs < n_blocks ? (sp.len + bs - 1) / bs : n_blocks;
+  __shared__ float red[256];
+  float best = 0.f;
+  const T* base = kbar + rh * n_blocks * D;
+  for (int64_t j = threadIdx.x; j < owned; j += blockDim.x) {
+    float ss = 0.f;
+    for (int64_t d = 0; d < D; ++d) {
+      float x = Elem<T>::load(base, j * D + d);
+      ss += x * x;
+    }
+    best = fmaxf(best, sqrtf(ss));  // fmaxf drops NaN; inf propagates
+  }
+  red[threadIdx.x] = best;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  // Slack for the float sum of squares and sqrtf (a few ulp).
+  if (threadIdx.x == 0) norm_out[rh] = red[0] * 1.0001f + 1e-30f;
+}
+
+// ---------------------------------------------------------------------------
+// Exact scoring helpers.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ inline float exact_score(const T* __restrict__ q, const T* __restrict__ kb, int D) {
+  double acc = 0.0;
+  for (int d = 0; d < D; ++d)
+    acc += static_cast<double>(Elem<T>::load(q, d)) * static_cast<double>(Elem<T>::load(kb, d));
+  return Elem<T>::round(static_cast<float>(acc));
+}
+
+// (s, j) ranks before (v, i) under (score desc, id asc).
+__device__ inline bool ranks_before(float s, int j, float v, int i) {
+  return s > v || (s == v && j < i);
+}
+
+// Inserts (s, j) into a list sorted by (score desc, id asc); the last entry
+// falls off. Entries with score -inf / NaN never enter.
+template <int M>
+__device__ inline void insert_exact(float (&val)[M], int (&idx)[M], float s, int j) {
+  bool carry = false;
+#pragma unroll
+  for (int p = 0; p < M; ++p) {
+    bool take = carry || ranks_before(s, j, val[p], idx[p]);
+    if (take) {
+      float tv = val[p]; int ti = idx[p];
+      val[p] = s; idx[p] = j;
+      s = tv; j = ti;
+      carry = true;
+    }
+  }
+}
+
+// Emits own block + selected ids ascending, -1 padded, into `out[0..slots)`.
+template <int M>
+__device__ inline void emit_sorted(int (&sel)[M], int n_sel, int own, bool cur,
+                                   int32_t* __restrict__ out, int slots) {
+  // Selected ids are distinct and all < own, so the own block goes last.
+  // Sort the first n_sel ascending (small insertion sort, static indices).
+#pragma unroll
+  for (int a = 1; a < M; ++a) {
+#pragma unroll
+    for (int b = a; b > 0; --b) {
+      if (b < n_sel && a < n_sel) {
+        int x = sel[b - 1], y = sel[b];
+        bool sw = x > y;
+        sel[b - 1] = sw ? y : x;
+        sel[b] = sw ? x : y;
+      }
+    }
+  }
+  int w = 0;
+#pragma unroll
+  for (int a = 0; a < M; ++a)
+    if (a < n_sel && w < slots) out[w++] = sel[a];
+  if (cur && w < slots) out[w++] = own;
+  for (; w < slots; ++w) out[w] = -1;
+}
+
+// Head-major index of query (r, hq, token) in [R*Hq, S] buffers.
+__device__ inline int64_t hm_query(bool packed, int64_t r, int64_t hq, int64_t h_q,
+                                   int64_t S, int64_t tok_global, int64_t t_local) {
+  return packed ? hq * S + tok_global : (r * h_q + hq) * S + t_local;
+}
+
+// ---------------------------------------------------------------------------
+// Exact kernel: one thread per query (or per queued query).
+// ---------------------------------------------------------------------------
+template <typename T, int TMAX>
+__global__ void __launch_bounds__(128)
+gate_exact_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
+                  int32_t* __restrict__ out, const int32_t* __restrict__ cu,
+                  int64_t S, int64_t rows_per_seq, int64_t h_q, int64_t h_kv,
+                  int D, int64_t n_blocks, int bs, int take, int cur, int slots,
+                  const int64_t* __restrict__ queue, const int* __restrict__ queue_len) {
+  const int64_t group = h_q / h_kv;
+  const bool packed = cu != nullptr;
+  int64_t total;
+  if (queue) total = *queue_len;
+  else total = static_cast<int64_t>(gridDim.y) * rows_per_seq;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x * (queue ? gridDim.y : 1);
+  int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (queue) first += static_cast<int64_t>(blockIdx.y) * gridDim.x * blockDim.x;
+  for (int64_t item = first; item < total; item += stride) {
+    int64_t r, hq, t;
+    if (queue) {
+      int64_t code = queue[item];  // (r * h_q + hq) * rows_per_seq + t
+      t = code % rows_per_seq;
+      int64_t rh = code / rows_per_seq;
+      r = rh / h_q;
+      hq = rh % h_q;
+    } else {
+      int64_t rh = blockIdx.y;
+      r = rh / h_q;
+      hq = rh % h_q;
+      t = item;
+      if (t >= rows_per_seq) break;
+    }
+    SeqSpan sp = seq_span(cu, r, S);
+    if (t >= sp.len) continue;
+    const int64_t tok = sp.bos + t;
+    const T* qrow = q + (tok * h_q + hq) * D;
+    const T* kb = kbar + (r * h_kv + hq / group) * n_blocks * D;
+    const int own = static_cast<int>(t / bs);
+    float val[TMAX];
+    int idx[TMAX];
+#pragma unroll
+    for (int p = 0; p < TMAX; ++p) { val[p] = -INFINITY; idx[p] = 0x7fffffff; }
+    if (take > 0) {
+      for (int j = 0; j < own; ++j) {
+        float s = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
+        if (!(s > val[take - 1 < TMAX ? take - 1 : TMAX - 1])) {
+          // cheap reject: cannot beat the current T-th best (ties lose to
+          // the earlier, lower id)
+          continue;
+        }
+        insert_exact<TMAX>(val, idx, s, j);
+      }
+    }
+    int n_sel = 0;
+#pragma unroll
+    for (int p = 0; p < TMAX; ++p)
+      if (p < take && val[p] > -INFINITY) n_sel = p + 1;
+    int32_t* o = out + hm_query(packed, r, hq, h_q, S, tok, t) * slots;
+    emit_sorted<TMAX>(idx, n_sel, own, cur != 0, o, slots);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA kernel (bf16 / fp16).
+// ---------------------------------------------------------------------------
+template <typename T> struct MfmaOps;
+template <> struct MfmaOps<bf16_t> {
+  typedef bf16x8_t vec;
+  __device__ static floatx16_t mfma(vec a, vec b, floatx16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static constexpr float kGapRel = 0.015625f;  // 2^-6 >= 2 bf16 ulps relative
+  static constexpr float kGapAbs = 1e-30f;
+  static constexpr float kMaxFinite = 3.0e38f;
+};
+template <> struct MfmaOps<f16_t> {
+  typedef f16x8_t vec;
+  __device__ static floatx16_t mfma(vec a, vec b, floatx16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static constexpr float kGapRel = 0.015625f;
+  static constexpr float kGapAbs = 2.0e-7f;    // > 2 fp16 subnormal spacings
+  static constexpr float kMaxFinite = 60000.f;  // beyond: fp16 rounds to inf
+};
+
+template <typename V>
+__device__ inline V load_vec16(const void* p) {
+  uint4 u = *reinterpret_cast<const uint4*>(p);
+  return __builtin_bit_cast(V, u);
+}
+
+template <typename T, int D, int M, int CAP, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64)
+gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
+                 int32_t* __restrict__ out, const int32_t* __restrict__ cu,
+                 int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
+                 int take, int cur, int slots, const float* __restrict__ kbar_norm,
+                 int64_t* __restrict__ queue, int* __restrict__ queue_len,
+                 int64_t rows_per_seq) {
+  using Ops = MfmaOps<T>;
+  using V = typename Ops::vec;
+  constexpr int KSTEPS = D / 16;
+  __shared__ float s_val[WAVES][CAP][64];
+  __shared__ int s_idx[WAVES][CAP][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const bool packed = cu != nullptr;
+
+  const int64_t rh = blockIdx.y;
+  const int64_t r = rh / h_q;
+  const int64_t hq = rh % h_q;
+  const int64_t hk = hq / (h_q / h_kv);
+  const SeqSpan sp = seq_span(cu, r, S);
+  // Tiles are numbered from the end so the longest ones start first.
+  const int64_t n_tiles = (rows_per_seq + 32 * WAVES - 1) / (32 * WAVES);
+  const int64_t tile = n_tiles - 1 - blockIdx.x;
+  const int64_t t0 = tile * 32 * WAVES + wave * 32;
+  if (t0 >= sp.len) return;
+  const int64_t t = t0 + col;
+  const bool live = t < sp.len;
+  const int own = live ? static_cast<int>(t / bs) : 0;
+  const int64_t last_t = (t0 + 31 < sp.len ? t0 + 31 : sp.len - 1);
+  const int horizon = static_cast<int>(last_t / bs);  // candidates are < own
+  const T* kb = kbar + (r * h_kv + hk) * n_blocks * D;
+  const int64_t tok = sp.bos + (live ? t : t0);
+  const T* qrow = q + (tok * h_q + hq) * D;
+
+  float lv[M];
+  int li[M];
+#pragma unroll
+  for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
+  int n_in_list = 0;
+
+  if (take > 0 && horizon > 0) {
+    // B operand: this lane's query, features 16c + 8*half + [0, 8).
+    V bq[KSTEPS];
+#pragma unroll
+    for (int c = 0; c < KSTEPS; ++c) {
+      if (live) bq[c] = load_vec16<V>(qrow + 16 * c + 8 * half);
+      else bq[c] = V{};
+    }
+    float thr = -INFINITY;
+    int cnt = 0;
+    const int n_chunks = (horizon + 31) / 32;
+    for (int ch = 0; ch < n_chunks; ++ch) {
+      const int blk0 = ch * 32;
+      const int arow = blk0 + col;  // A row this lane supplies
+      floatx16_t acc = {};
+      if (arow < horizon) {
+        const T* ap = kb + static_cast<int64_t>(arow) * D + 8 * half;
+#pragma unroll
+        for (int c = 0; c < KSTEPS; ++c)
+          acc = Ops::mfma(load_vec16<V>(ap + 16 * c), bq[c], acc);
+      } else {
+#pragma unroll
+        for (int c = 0; c < KSTEPS; ++c) acc = Ops::mfma(V{}, bq[c], acc);
+      }
+      // acc[v] is the score of block blk0 + 8*(v/4) + 4*half + v%4.
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int b = blk0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        const float a = (b < own) ? acc[v] : -INFINITY;
+        if (a > thr) {
+          s_val[wave][cnt][lane] = a;
+          s_idx[wave][cnt][lane] = b;
+          ++cnt;
+        }
+      }
+      // Fold buffers that could overflow on the next chunk.
+      if (__any(cnt > CAP - 16)) {
+        for (int e = 0; e < cnt; ++e) {
+          const float s = s_val[wave][e][lane];
+          const int j = s_idx[wave][e][lane];
+          if (s > lv[M - 1]) insert_exact<M>(lv, li, s, j);
+        }
+        cnt = 0;
+        thr = lv[M - 1];
+      }
+    }
+    for (int e = 0; e < cnt; ++e) {
+      const float s = s_val[wave][e][lane];
+      const int j = s_idx[wave][e][lane];
+      if (s > lv[M - 1]) insert_exact<M>(lv, li, s, j);
+    }
+#pragma unroll
+    for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
+  }
+
+  // --- Merge the two half-lists of this query and decide. -----------------
+  // Rejected candidates of a lane are all <= its M-th best when its list is
+  // full, and there are none otherwise.
+  const float rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
+  const float rej_other = __shfl_xor(rej_mine, 32);
+  const float rej = fmaxf(rej_mine, rej_other);
+  float pv[M];
+#pragma unroll
+  for (int p = 0; p < M; ++p) pv[p] = __shfl_xor(lv[p], 32);
+  // L = the take-th largest value of the union (a multiset): x is it when
+  // fewer than `take` values exceed x and at least `take` reach it.
+  float L = -INFINITY;
+  if (take > 0) {
+#pragma unroll
+    for (int p = 0; p < 2 * M; ++p) {
+      const float x = p < M ? lv[p] : pv[p - M];
+      int gt = 0, ge = 0;
+#pragma unroll
+      for (int u = 0; u < M; ++u) {
+        gt += (lv[u] > x) + (pv[u] > x);
+        ge += (lv[u] >= x) + (pv[u] >= x);
+      }
+      if (x > -INFINITY && gt < take && take <= ge) L = x;
+    }
+  }
+  // Error band of this query: E >= |approx - exact| for every candidate.
+  float qn = 0.f;
+  if (live && take > 0) {
+    for (int d = 0; d < D; ++d) {
+      float x = Elem<T>::load(qrow, d);
+      qn += x * x;
+    }
+  }
+  const float E = ldexpf(sqrtf(qn) * 1.0001f * kbar_norm[r * h_kv + hk], -14) + 1e-37f;
+  bool ok = true;
+  float cut = -INFINITY;
+  if (take > 0 && L > -INFINITY) {
+    const float mag = fmaxf(fabsf(L), fabsf(rej == -INFINITY ? 0.f : rej)) + E;
+    const float gap = Ops::kGapRel * mag + Ops::kGapAbs;
+    if (!(mag < Ops::kMaxFinite)) ok = false;
+    if (rej > -INFINITY && !(L - rej > 2.f * E + gap)) ok = false;
+    cut = L - 2.f * E - gap;
+  }
+  if (take > 0 && !(E < INFINITY)) ok = false;  // q or kbar carries inf / NaN
+  // Exact rescoring of the surviving candidates of this lane's half.
+  float ev[M];
+  int ei[M];
+#pragma unroll
+  for (int p = 0; p < M; ++p) { ev[p] = -INFINITY; ei[p] = 0x7fffffff; }
+  if (ok && take > 0 && live) {
+#pragma unroll
+    for (int p = 0; p < M; ++p) {
+      if (lv[p] > -INFINITY && lv[p] >= cut) {
+        float s = exact_score(qrow, kb + static_cast<int64_t>(li[p]) * D, D);
+        if (s > -INFINITY) insert_exact<M>(ev, ei, s, li[p]);
+      }
+    }
+  }
+  // Merge with the partner's exact list.
+  float fv[M];
+  int fi[M];
+#pragma unroll
+  for (int p = 0; p < M; ++p) { fv[p] = ev[p]; fi[p] = ei[p]; }
+#pragma unroll
+  for (int p = 0; p < M; ++p) {
+    const float s = __shfl_xor(ev[p], 32);
+    const int j = __shfl_xor(ei[p], 32);
+    if (s > -INFINITY) insert_exact<M>(fv, fi, s, j);
+  }
+  const int ok_all = (ok ? 1 : 0) & __shfl_xor(ok ? 1 : 0, 32);
+  if (!live || half != 0) return;
+  const int64_t qid = hm_query(packed, r, hq, h_q, S, tok, t);
+  if (!ok_all) {
+    const int slot = atomicAdd(queue_len, 1);
+    queue[slot] = (r * h_q + hq) * rows_per_seq + t;
+    return;
+  }
+  int n_sel = 0;
+#pragma unroll
+  for (int p = 0; p < M; ++p)
+    if (p < take && fv[p] > -INFINITY) n_sel = p + 1;
+  emit_sorted<M>(fi, n_sel, own, cur != 0, out + qid * slots, slots);
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers.
+// ---------------------------------------------------------------------------
+template <typename T, int TMAX>
+static int launch_exact(const void* q, const void* kbar, int32_t* out,
+                        const int32_t* cu, const Geometry& g, int take, int cur,
+                        const int64_t* queue, const int* queue_len, hipStream_t st) {
+  if (queue) {
+    dim3 grid(512, 1);
+    hipLaunchKernelGGL((gate_exact_kernel<T, TMAX>), grid, dim3(128), 0, st,
+                       static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
+                       g.seq_len, g.rows_per_seq, g.h_q, g.h_kv,
+                       static_cast<int>(g.head_dim), g.n_blocks,
+                       static_cast<int>(g.block_size), take, cur,
+                       static_cast<int>(g.slots), queue, queue_len);
+  } else {
+    dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq, 128)),
+              static_cast<unsigned>(g.rows * g.h_q));
+    hipLaunchKernelGGL((gate_exact_kernel<T, TMAX>), grid, dim3(128), 0, st,
+                       static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
+                       g.seq_len, g.rows_per_seq, g.h_q, g.h_kv,
+                       static_cast<int>(g.head_dim), g.n_blocks,
+                       static_cast<int>(g.block_size), take, cur,
+                       static_cast<int>(g.slots), nullptr, nullptr);
+  }
+  return check_launch("moba_gate (exact)");
+}
+
+template <typename T>
+static int dispatch_exact(const void* q, const void* kbar, int32_t* out,
+                          const int32_t* cu, const Geometry& g, int take, int cur,
+                          const int64_t* queue, const int* queue_len, hipStream_t st) {
+  if (take <= 8) return launch_exact<T, 8>(q, kbar, out, cu, g, take, cur, queue, queue_len, st);
+  if (take <= 16) return launch_exact<T, 16>(q, kbar, out, cu, g, take, cur, queue, queue_len, st);
+  if (take <= 32) return launch_exact<T, 32>(q, kbar, out, cu, g, take, cur, queue, queue_len, st);
+  if (take <= 64) return launch_exact<T, 64>(q, kbar, out, cu, g, take, cur, queue, queue_len, st);
+  if (take <= 128) return launch_exact<T, 128>(q, kbar, out, cu, g, take, cur, queue, queue_len, st);
+  return fail(MOBA_ERR_UNSUPPORTED, "gate supports at most 128 past blocks per query");
+}
+
+template <typename T, int D, int M>
+static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int32_t* cu,
+                       const Geometry& g, int take, int cur, const GateWs& ws,
+                       hipStream_t st) {
+  constexpr int WAVES = 4;
+  constexpr int CAP = M + 24;
+  dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq, 32 * WAVES)),
+            static_cast<unsigned>(g.rows * g.h_q));
+  hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, CAP, WAVES>), grid, dim3(64 * WAVES), 0, st,
+                     static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
+                     g.seq_len, g.h_q, g.h_kv, g.n_blocks, static_cast<int>(g.block_size),
+                     take, cur, static_cast<int>(g.slots), ws.kbar_norm, ws.queue,
+                     ws.counter, g.rows_per_seq);
+  return check_launch("moba_gate (mfma)");
+}
+
+template <typename T>
+static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t* cu,
+                    const Geometry& g, int take, int cur, void* workspace,
+                    size_t ws_bytes, hipStream_t st) {
+  if constexpr (Elem<T>::kCode == MOBA_FP32) {
+    (void)workspace; (void)ws_bytes;
+    return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, nullptr, nullptr, st);
+  } else {
+  const bool mfma_ok = (g.head_dim == 64 || g.head_dim == 128) && take <= 16;
+  if (!mfma_ok) return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, nullptr, nullptr, st);
+  const int64_t qcap = g.rows * g.h_q * g.rows_per_seq;
+  if (!workspace || ws_bytes < moba_gate_workspace_size(g.rows, g.rows_per_seq, g.h_q) ||
+      ws_bytes < 256 + align256(sizeof(float) * g.rows * g.h_kv) + sizeof(int64_t) * qcap)
+    return fail(MOBA_ERR_WORKSPACE, "gate workspace too small");
+  GateWs ws = gate_ws(workspace, g.rows, g.h_kv, qcap);
+  hipLaunchKernelGGL(gate_prep_kernel<T>, dim3(static_cast<unsigned>(g.rows * g.h_kv)),
+                     dim3(256), 0, st, static_cast<const T*>(kbar), cu, g.seq_len,
+                     g.h_kv, g.n_blocks, g.head_dim, g.block_size, ws.kbar_norm,
+                     ws.counter);
+  int rc = check_launch("moba_gate (prep)");
+  if (rc) return rc;
+  if (g.head_dim == 64) {
+    rc = take <= 8 ? launch_mfma<T, 64, 8>(q, kbar, out, cu, g, take, cur, ws, st)
+                   : launch_mfma<T, 64, 16>(q, kbar, out, cu, g, take, cur, ws, st);
+  } else {
+    rc = take <= 8 ? launch_mfma<T, 128, 8>(q, kbar, out, cu, g, take, cur, ws, st)
+                   : launch_mfma<T, 128, 16>(q, kbar, out, cu, g, take, cur, ws, st);
+  }
+  if (rc) return rc;
+  // Queries whose approximate evidence was insufficient: exact rescoring.
+  return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, ws.queue, ws.counter, st);
+  }
+}
+
+}  // namespace moba
+
+extern "C" size_t moba_gate_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q) {
+  // counter + norms (bounded by batch * h_q floats) + one queue entry per query.
+  size_t norms = (sizeof(float) * batch * h_q + 255) & ~size_t(255);
+  return 256 + norms + sizeof(int64_t) * static_cast<size_t>(batch * h_q * seq_len);
+}
+
+extern "C" int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
+                         const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+                         int64_t max_seqlen, int64_t h_q, int64_t h_kv,
+                         int64_t head_dim, int64_t n_blocks, int64_t block_size,
+                         int64_t slots, int64_t take, int always_current, int dtype,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace moba;
+  Geometry g;
+  int st = make_geometry(&g, batch, seq_len, max_seqlen, h_q, h_kv, head_dim, n_blocks,
+                         block_size, slots, cu_seqlens);
+  if (st) return st;
+  if (!q || !kbar || !block_idx) return fail(MOBA_ERR_INVALID, "null pointer");
+  if (take < 0 || slots < take + (always_current ? 1 : 0))
+    return fail(MOBA_ERR_INVALID, "slots must hold take (+1 with the own block)");
+  if (g.rows_per_seq >= (int64_t(1) << 31) / 2)
+    return fail(MOBA_ERR_UNSUPPORTED, "sequence too long for int32 block ids");
+  return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
+    return run_gate<T>(q, kbar, block_idx, cu_seqlens, g, static_cast<int>(take),
+                       always_current ? 1 : 0, workspace, workspace_bytes,
+                       as_stream(stream));
+  });
+}

@@ -1,0 +1,141 @@
+"""KV-block-major forward (reference `src/moba/kernels/moba_fwd.py`).
+
+`attend_partials` runs one program per (KV block, kv head): the block's keys
+against every query that selected it, writing per-slot un-normalised
+partials (m in log2 units, l, acc). `combine_partials` merges each query's
+slots. Both run the HIP library.
+"""
+
+import torch
+
+from moba import _lib
+from moba.config import MoBAConfig
+from moba.device import TENSOR_CORE_TILE, check_gathered_head_dim
+from moba.gqa import head_group_size
+from moba.kernels.routing import CSCIndex, build_csc_fused
+from moba.varlen import validate_cu_seqlens
+
+
+def empty_partials(shape, slots: int, device, partials_dtype=torch.float32):
+    """Uninitialised head-major partial buffers for a token-major query
+    shape (`moba_fwd.py:529-563`): part_m, part_l [B, H, S, K] fp32 and
+    part_acc [B, H, S, K, D] in `partials_dtype`."""
+    b, s, h, d = shape
+    return (torch.empty((b, h, s, slots), device=device, dtype=torch.float32),
+            torch.empty((b, h, s, slots), device=device, dtype=torch.float32),
+            torch.empty((b, h, s, slots, d), device=device, dtype=partials_dtype))
+
+
+def _rows(index: CSCIndex, b: int) -> int:
+    return index.col_nnz.shape[0]
+
+
+def attend_partials(q, k, v, cfg: MoBAConfig, index: CSCIndex, causal: bool = True,
+                    partials_dtype=None, partials=None):
+    """The attention stage, returning un-merged partials (`moba_fwd.py:566-665`).
+
+    part_m is reset to -inf inside the library call (the written-marker);
+    part_l / part_acc of unwritten slots are never read.
+    """
+    b, s, h_q, d = q.shape
+    h_kv = k.shape[2]
+    dev = _lib.require_gpu(q, k, v)
+    slots = index.max_slots
+    if partials_dtype is None:
+        partials_dtype = q.dtype
+    if partials is None:
+        partials = empty_partials(q.shape, slots, dev, partials_dtype)
+    part_m, part_l, part_acc = partials
+    q, k, v = (_lib.aligned_contiguous(t) for t in (q, k, v))
+    rows = _rows(index, b)
+    mx = index.max_seqlen if index.cu_seqlens is not None else s
+    _lib.call("moba_attend", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
+              _lib.ptr(index.col_nnz), _lib.ptr(index.col_offsets),
+              _lib.ptr(index.row_indices), _lib.ptr(index.head_indices),
+              _lib.ptr(index.slot_of_pair), _lib.ptr(index.order),
+              _lib.ptr(part_m), _lib.ptr(part_l), _lib.ptr(part_acc),
+              _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d,
+              index.num_blocks, cfg.block_size, slots, index.row_indices.shape[-1],
+              int(bool(causal)), _lib.DTYPE_CODE[q.dtype],
+              _lib.DTYPE_CODE[part_acc.dtype], _lib.stream_handle(dev))
+    return part_m, part_l, part_acc
+
+
+def combine_partials(part_m, part_l, part_acc, out_dtype, block_m=None,
+                     return_lse: bool = False):
+    """Merges per-slot partials into the output (`moba_fwd.py:668-725`).
+
+    Returns:
+        out [B, S, H, D] (`out_dtype`), plus lse [B, H, S] fp32 in log2
+        units when `return_lse`.
+
+    Raises:
+        ValueError: If the buffers disagree on shape.
+    """
+    del block_m  # the HIP merge has a fixed tile
+    b, h, s, slots = part_m.shape
+    d = part_acc.shape[-1]
+    if part_l.shape != part_m.shape:
+        raise ValueError(f"shape mismatch: part_l {tuple(part_l.shape)} against "
+                         f"part_m {tuple(part_m.shape)}")
+    if part_acc.shape != (b, h, s, slots, d):
+        raise ValueError(f"shape mismatch: part_acc {tuple(part_acc.shape)} against "
+                         f"{(b, h, s, slots, d)}")
+    dev = _lib.require_gpu(part_m, part_l, part_acc)
+    part_m, part_l, part_acc = (t.contiguous() for t in (part_m, part_l, part_acc))
+    if part_m.dtype != torch.float32 or part_l.dtype != torch.float32:
+        part_m, part_l = part_m.float(), part_l.float()
+    out = torch.empty((b, s, h, d), device=dev, dtype=out_dtype)
+    lse = torch.empty((b, h, s), device=dev, dtype=torch.float32) if return_lse else None
+    _lib.call("moba_combine", _lib.ptr(part_m), _lib.ptr(part_l), _lib.ptr(part_acc),
+              _lib.ptr(out), _lib.ptr(lse), b, s, h, d, slots,
+              _lib.DTYPE_CODE[part_acc.dtype], _lib.DTYPE_CODE[out_dtype],
+              _lib.stream_handle(dev))
+    return (out, lse) if return_lse else out
+
+
+def _validate(q, k, v, cfg: MoBAConfig, cu_seqlens=None, max_seqlen=None) -> None:
+    """Shape and configuration checks before any launch (`moba_fwd.py:733-780`).
+
+    Raises:
+        ValueError: On mismatched shapes, indivisible heads, bad packing
+            metadata, an unsupported head_dim or dtype, or block_size < 16.
+    """
+    if k.shape != v.shape:
+        raise ValueError(f"key/value shape mismatch: {k.shape}, {v.shape}")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"shape mismatch: {q.shape}, {k.shape}, {v.shape}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"dtype mismatch: {q.dtype}, {k.dtype}, {v.dtype}")
+    head_group_size(q.shape[2], k.shape[2])
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError(f"packed input must have batch 1, got {q.shape[0]}")
+        if max_seqlen is None:
+            raise ValueError("max_seqlen is required when cu_seqlens is given")
+        validate_cu_seqlens(cu_seqlens, total_tokens=q.shape[1], max_seqlen=max_seqlen)
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise ValueError(f"unsupported dtype {q.dtype}")
+    ok, reason = check_gathered_head_dim(q.shape[-1], q.element_size())
+    if not ok:
+        raise ValueError(reason)
+    if q.shape[-1] > 128:
+        raise ValueError(f"head_dim {q.shape[-1]} above 128 is not supported")
+    if cfg.block_size < TENSOR_CORE_TILE:
+        raise ValueError(f"block_size {cfg.block_size} below the MFMA tile minimum "
+                         f"of {TENSOR_CORE_TILE}")
+
+
+def moba_forward(q, k, v, cfg: MoBAConfig, index: CSCIndex | None = None,
+                 causal: bool = True, partials_dtype=None, cu_seqlens=None,
+                 max_seqlen=None):
+    """MoBA attention forward, no autograd (`moba_fwd.py:783-835`)."""
+    if index is not None:
+        cu_seqlens, max_seqlen = index.cu_seqlens, index.max_seqlen
+    _validate(q, k, v, cfg, cu_seqlens, max_seqlen)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if index is None:
+        index = build_csc_fused(q, k, cfg, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+    part_m, part_l, part_acc = attend_partials(q, k, v, cfg, index, causal=causal,
+                                               partials_dtype=partials_dtype)
+    return combine_partials(part_m, part_l, part_acc, q.dtype)

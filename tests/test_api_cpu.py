@@ -1,0 +1,98 @@
+"""Host-side API behaviour that needs no GPU: config semantics, the backend
+registry contract, validation errors, and the no-CPU-fallback rule."""
+
+import pytest
+import torch
+
+import implementations
+from implementations.base import Backend, get_backend, register
+from moba.config import MoBAConfig
+from moba.gqa import expand_kv, head_group_size
+from moba.kernels.moba_fwd import _validate, moba_forward
+from moba.varlen import validate_cu_seqlens
+
+
+def test_config_defaults_and_budget():
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    assert cfg.dtype is torch.bfloat16
+    assert cfg.always_select_current and cfg.top_k_includes_current
+    assert cfg.tie_break_low_index and not cfg.pool_masked_only
+    assert cfg.past_blocks_selected(512) == 7
+    assert cfg.past_blocks_selected(3) == 3
+    assert cfg.num_blocks(1000) == 8
+    assert cfg.slots() == 8
+    assert MoBAConfig(32, 3, top_k_includes_current=False).slots() == 4
+    assert MoBAConfig(32, 3, always_select_current=False).slots() == 3
+    with pytest.raises(ValueError):
+        MoBAConfig(block_size=0, top_k=1)
+    with pytest.raises(ValueError):
+        MoBAConfig(block_size=16, top_k=0)
+    with pytest.raises(Exception):
+        cfg.top_k = 3  # frozen
+
+
+def test_head_group_and_expand():
+    assert head_group_size(32, 8) == 4
+    with pytest.raises(ValueError):
+        head_group_size(6, 4)
+    t = torch.arange(2 * 3).view(1, 1, 2, 3)
+    e = expand_kv(t, 4)
+    assert torch.equal(e[0, 0, :, 0], torch.tensor([0, 0, 3, 3]))
+
+
+def test_registry_contract():
+    names = [b.name for b in implementations.all_backends()]
+    assert "ours" in names and "triton_moba" in names
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    for b in implementations.all_backends():
+        assert isinstance(b, Backend)
+        ok, reason = b.is_available(cfg)  # never raises
+        assert isinstance(ok, bool) and isinstance(reason, str)
+        if not torch.cuda.is_available():
+            assert not ok and reason
+    with pytest.raises(ValueError):
+        register(get_backend("ours"))
+    with pytest.raises(KeyError, match="ours"):
+        get_backend("nope")
+
+
+def test_validation_errors():
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    q = torch.zeros(1, 256, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="key/value"):
+        _validate(q, q, q[:, :, :2], cfg)
+    with pytest.raises(ValueError, match="divisible"):
+        _validate(q, q[:, :, :3], q[:, :, :3], cfg)
+    with pytest.raises(ValueError, match="power of two"):
+        z = torch.zeros(1, 256, 4, 96, dtype=torch.bfloat16)
+        _validate(z, z, z, cfg)
+    with pytest.raises(ValueError, match="cache line"):
+        z = torch.zeros(1, 256, 4, 32, dtype=torch.bfloat16)
+        _validate(z, z, z, cfg)
+    with pytest.raises(ValueError, match="block_size"):
+        _validate(q, q, q, MoBAConfig(block_size=8, top_k=2))
+    with pytest.raises(ValueError, match="max_seqlen"):
+        _validate(q, q, q, cfg, cu_seqlens=torch.tensor([0, 256], dtype=torch.int32))
+
+
+def test_cu_seqlens_validation():
+    good = torch.tensor([0, 80, 128, 212], dtype=torch.int32)
+    assert validate_cu_seqlens(good, 212, 84) == 3
+    with pytest.raises(ValueError, match="int32"):
+        validate_cu_seqlens(good.long(), 212, 84)
+    with pytest.raises(ValueError, match="start at 0"):
+        validate_cu_seqlens(torch.tensor([1, 212], dtype=torch.int32), 212, 300)
+    with pytest.raises(ValueError, match="increasing"):
+        validate_cu_seqlens(torch.tensor([0, 80, 80, 212], dtype=torch.int32), 212, 200)
+    with pytest.raises(ValueError, match="ends at"):
+        validate_cu_seqlens(good, 300, 84)
+    with pytest.raises(ValueError, match="below the longest"):
+        validate_cu_seqlens(good, 212, 50)
+
+
+def test_no_cpu_fallback():
+    """The product path never computes on the CPU: CPU tensors are refused."""
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    q = torch.zeros(1, 256, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        moba_forward(q, q, q, cfg)

@@ -1,0 +1,222 @@
+"""Forward, merge and backward on the GPU against the fp64 oracle."""
+
+import math
+
+import pytest
+import torch
+
+from conftest import make_qkv, oracle_cfg
+from gpu_util import fp64_truth, oracle_selection, to_cpu
+from moba.config import MoBAConfig
+from moba.kernels.attention import moba_attention
+from moba.kernels.moba_fwd import combine_partials, moba_forward
+from moba.kernels.routing import build_csc_fused, csc_to_mask
+from oracle import naive as O
+from tolerance import (BF16_MAX_ABS, BF16_MEAN_ABS, FP32_MAX_ABS, assert_selection_matches,
+                       assert_within_tolerance, max_abs_error, mean_abs_error)
+
+pytestmark = pytest.mark.gpu
+
+FWD_CASES = [
+    # (shape, h_kv, block_size, top_k)
+    ((1, 1024, 4, 128), 4, 64, 8),
+    ((2, 1024, 4, 64), 4, 32, 4),
+    ((1, 2048, 4, 64), 4, 128, 8),
+    ((1, 1000, 2, 64), 2, 128, 5),
+    ((1, 2048, 8, 128), 2, 64, 4),
+    ((1, 1024, 4, 64), 1, 64, 3),
+]
+
+
+@pytest.mark.parametrize("shape,h_kv,bs,tk", FWD_CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_forward_within_tolerance(device, shape, h_kv, bs, tk, dtype):
+    cfg = MoBAConfig(block_size=bs, top_k=tk, dtype=dtype)
+    q, k, v = make_qkv(shape, dtype, seed=1, device=device)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    index = build_csc_fused(q, k, cfg)
+    sel = oracle_selection(q, k, cfg)
+    assert_selection_matches(csc_to_mask(index, shape[1]), sel, "ours")
+    out = moba_forward(q, k, v, cfg, index=index)
+    truth, ref_err = fp64_truth(q, k, v, cfg, sel)
+    assert_within_tolerance(out, truth, ref_err, "ours")
+    if dtype == torch.bfloat16:
+        assert max_abs_error(out, truth) <= BF16_MAX_ABS
+        assert mean_abs_error(out, truth) <= BF16_MEAN_ABS
+
+
+@pytest.mark.parametrize("shape,h_kv,bs,tk", [((1, 1024, 4, 64), 4, 64, 8),
+                                              ((1, 1024, 4, 128), 2, 128, 4),
+                                              ((1, 4096, 4, 64), 4, 128, 8)])
+def test_forward_fp32_matches_oracle(device, shape, h_kv, bs, tk):
+    cfg = MoBAConfig(block_size=bs, top_k=tk, dtype=torch.float32)
+    q, k, v = make_qkv(shape, torch.float32, seed=2, device=device)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    out = moba_forward(q, k, v, cfg)
+    sel = oracle_selection(q, k, cfg)
+    truth, _ = fp64_truth(q, k, v, cfg, sel)
+    assert max_abs_error(out, truth) <= FP32_MAX_ABS
+
+
+def test_forward_packed_equals_each_sequence_alone(device):
+    cfg = MoBAConfig(block_size=16, top_k=3)
+    lens = [80, 48, 64, 20]
+    cu = torch.tensor([0, 80, 128, 192, 212], dtype=torch.int32, device=device)
+    q, k, v = make_qkv((1, 212, 2, 64), torch.bfloat16, seed=5, device=device)
+    packed = moba_forward(q, k, v, cfg, cu_seqlens=cu, max_seqlen=80)
+    for r, ln in enumerate(lens):
+        lo = int(cu[r])
+        alone = moba_forward(q[:, lo:lo + ln], k[:, lo:lo + ln], v[:, lo:lo + ln], cfg)
+        assert torch.equal(packed[:, lo:lo + ln], alone), f"sequence {r}"
+    sel = oracle_selection(q, k, cfg, cu_seqlens=cu)
+    truth, ref_err = fp64_truth(q, k, v, cfg, sel, cu_seqlens=cu)
+    assert_within_tolerance(packed, truth, ref_err, "packed")
+
+
+def test_forward_is_deterministic_and_routing_fixed_by_index(device):
+    cfg = MoBAConfig(block_size=64, top_k=4)
+    q, k, v = make_qkv((1, 2048, 2, 64), torch.bfloat16, seed=7, device=device)
+    index = build_csc_fused(q, k, cfg)
+    a = moba_forward(q, k, v, cfg, index=index)
+    b = moba_forward(q, k, v, cfg, index=index)
+    assert torch.equal(a, b)
+    c = moba_forward(q, k, v, cfg)
+    assert torch.equal(a, c), "forward depends on column order"
+
+
+def reference_combine_inputs(device, b=1, h=2, s=33, slots=5, d=64, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(0)
+    m = torch.randn(b, h, s, slots, generator=g) * 4
+    l = torch.rand(b, h, s, slots, generator=g) * 3 + 0.5
+    acc = torch.randn(b, h, s, slots, d, generator=g)
+    return m, l, acc
+
+
+@pytest.mark.parametrize("slots", [1, 3, 5, 8, 12])
+def test_combine_matches_textbook_merge(device, slots):
+    m, l, acc = reference_combine_inputs(device, slots=slots)
+    acc_b = acc.to(torch.bfloat16)
+    out, lse = combine_partials(m.to(device), l.to(device), acc_b.to(device), torch.float32,
+                                return_lse=True)
+    ref_out, ref_lse = O.combine_reference(m.double(), l.double(), acc_b.double())
+    assert max_abs_error(out, ref_out) < 1e-5
+    assert max_abs_error(lse, ref_lse) < 1e-5
+
+
+def test_combine_ignores_unwritten_slots_holding_nan(device):
+    m, l, acc = reference_combine_inputs(device, slots=4)
+    m[..., 2] = float("-inf")
+    l[..., 2] = float("nan")
+    acc[..., 2, :] = float("nan")
+    out = combine_partials(m.to(device), l.to(device), acc.to(device), torch.float32)
+    assert bool(torch.isfinite(out).all())
+    ref, _ = O.combine_reference(m.double(), l.double(), acc.double())
+    assert max_abs_error(out, ref) < 1e-5
+
+
+def test_combine_shift_invariance_and_dominant_slot(device):
+    m, l, acc = reference_combine_inputs(device, slots=4, dtype=torch.float32)
+    out1 = combine_partials(m.to(device), l.to(device), acc.to(device), torch.float32)
+    out2 = combine_partials((m + 37.0).to(device), l.to(device), acc.to(device), torch.float32)
+    assert max_abs_error(out1, out2) < 1e-5
+    m2 = m.clone()
+    m2[..., 0] = 500.0
+    out3 = combine_partials(m2.to(device), l.to(device), acc.to(device), torch.float32)
+    ref = (acc[..., 0, :] / l[..., 0:1]).permute(0, 2, 1, 3)
+    assert max_abs_error(out3, ref) < 1e-5
+
+
+def grads_oracle(q, k, v, cfg, sel, g, dtype=torch.float64):
+    qc, kc, vc, gc = (t.detach().cpu().to(dtype).requires_grad_(True) for t in (q, k, v, g))
+    out = O.moba_attention(qc, kc, vc, oracle_cfg(cfg), selected=sel, query_chunk=256)
+    out.backward(gc.detach())
+    return qc.grad, kc.grad, vc.grad
+
+
+BWD_CASES = [((1, 512, 2, 64), 2, 64, 4), ((1, 1024, 2, 128), 2, 128, 4),
+             ((1, 1024, 4, 64), 2, 64, 3), ((2, 640, 2, 64), 2, 32, 6)]
+
+
+@pytest.mark.parametrize("shape,h_kv,bs,tk", BWD_CASES)
+def test_backward_within_tolerance(device, shape, h_kv, bs, tk):
+    cfg = MoBAConfig(block_size=bs, top_k=tk)
+    q, k, v = make_qkv(shape, torch.bfloat16, seed=3, device=device)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    g = make_qkv(shape, torch.bfloat16, seed=4, device=device, n=1)[0]
+    sel = oracle_selection(q, k, cfg)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = moba_attention(qq, kk, vv, cfg)
+    out.backward(g)
+    truth = grads_oracle(q, k, v, cfg, sel, g)
+    low = grads_oracle(q, k, v, cfg, sel, g, dtype=torch.bfloat16)
+    for name, ours, ref, tr in [("dq", qq.grad, low[0], truth[0]), ("dk", kk.grad, low[1], truth[1]),
+                                ("dv", vv.grad, low[2], truth[2])]:
+        ref_err = max_abs_error(ref, tr)
+        assert_within_tolerance(ours, tr, ref_err, name)
+        assert max_abs_error(ours, tr) <= BF16_MAX_ABS, name
+        assert mean_abs_error(ours, tr) <= BF16_MEAN_ABS, name
+
+
+def test_backward_fp32_matches_autograd(device):
+    cfg = MoBAConfig(block_size=64, top_k=4, dtype=torch.float32)
+    shape = (1, 512, 2, 64)
+    q, k, v = make_qkv(shape, torch.float32, seed=3, device=device)
+    g = make_qkv(shape, torch.float32, seed=4, device=device, n=1)[0]
+    sel = oracle_selection(q, k, cfg)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    moba_attention(qq, kk, vv, cfg).backward(g)
+    truth = grads_oracle(q, k, v, cfg, sel, g)
+    for ours, tr in zip((qq.grad, kk.grad, vv.grad), truth):
+        assert max_abs_error(ours, tr) <= FP32_MAX_ABS
+
+
+def test_unselected_blocks_get_exactly_zero_gradient(device):
+    cfg = MoBAConfig(block_size=64, top_k=2, always_select_current=False)
+    shape = (1, 1024, 2, 64)
+    q, k, v = make_qkv(shape, torch.bfloat16, device=device)
+    g = make_qkv(shape, torch.bfloat16, seed=9, device=device, n=1)[0] * 0.1
+    index = build_csc_fused(q, k, cfg)
+    empty = index.col_nnz == 0
+    assert bool(empty.any())
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = moba_attention(qq, kk, vv, cfg, index=index)
+    out = torch.nan_to_num(out)  # queries with no selection produce NaN by design
+    out.backward(g)
+    for b, h, blk in empty.nonzero().tolist():
+        lo, hi = blk * 64, min(blk * 64 + 64, 1024)
+        assert not bool(kk.grad[b, lo:hi, h].any())
+        assert not bool(vv.grad[b, lo:hi, h].any())
+
+
+def test_backward_is_deterministic_given_an_index(device):
+    cfg = MoBAConfig(block_size=64, top_k=4)
+    shape = (1, 1024, 2, 64)
+    q, k, v = make_qkv(shape, torch.bfloat16, seed=11, device=device)
+    g = make_qkv(shape, torch.bfloat16, seed=12, device=device, n=1)[0]
+    index = build_csc_fused(q, k, cfg)
+    res = []
+    for _ in range(2):
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        moba_attention(qq, kk, vv, cfg, index=index).backward(g)
+        res.append((qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_packed_backward_equals_each_sequence_alone(device):
+    cfg = MoBAConfig(block_size=16, top_k=3)
+    lens = [80, 48, 64, 20]
+    cu = torch.tensor([0, 80, 128, 192, 212], dtype=torch.int32, device=device)
+    q, k, v = make_qkv((1, 212, 2, 64), torch.bfloat16, seed=5, device=device)
+    g = make_qkv((1, 212, 2, 64), torch.bfloat16, seed=6, device=device, n=1)[0]
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    moba_attention(qq, kk, vv, cfg, cu_seqlens=cu, max_seqlen=80).backward(g)
+    for r, ln in enumerate(lens):
+        lo = int(cu[r])
+        a = [t[:, lo:lo + ln].clone().requires_grad_(True) for t in (q, k, v)]
+        moba_attention(*a, cfg).backward(g[:, lo:lo + ln])
+        # dq is per query and exact; dk / dv sum down a column whose entry
+        # order is unspecified, so they may differ in the last bf16 bit.
+        assert torch.equal(qq.grad[:, lo:lo + ln], a[0].grad), f"dq, sequence {r}"
+        for ours, alone in zip((kk.grad, vv.grad), a[1:]):
+            assert max_abs_error(ours[:, lo:lo + ln], alone.grad) < 2e-2, f"sequence {r}"

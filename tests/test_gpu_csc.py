@@ -1,0 +1,86 @@
+"""The CSC transpose on the GPU against the oracle's reference builder."""
+
+import pytest
+import torch
+
+from conftest import make_qkv, oracle_cfg
+from moba.config import MoBAConfig
+from moba.kernels.routing import build_csc_from_indices, build_csc_fused, csc_to_mask
+from oracle import naive as O
+
+pytestmark = pytest.mark.gpu
+
+
+def column_sets(index, b, kv, blk):
+    lo = int(index.col_offsets[b, kv, blk])
+    n = int(index.col_nnz[b, kv, blk])
+    r = index.row_indices[b, kv, lo:lo + n].tolist()
+    h = index.head_indices[b, kv, lo:lo + n].tolist()
+    s = index.slot_of_pair[b, kv, lo:lo + n].tolist()
+    return sorted(zip(h, r, s))
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,bs,tk", [(1, 2048, 4, 4, 64, 8), (2, 1024, 4, 2, 32, 4),
+                                              (1, 4096, 8, 2, 128, 8), (1, 1000, 2, 1, 128, 5)])
+def test_csc_matches_reference_builder(device, b, s, hq, hkv, bs, tk):
+    cfg = MoBAConfig(block_size=bs, top_k=tk)
+    q, k, _ = make_qkv((b, s, hq, 64), torch.bfloat16, seed=1, device=device)
+    k = k[:, :, :hkv].contiguous()
+    index = build_csc_fused(q, k, cfg)
+    sel = O.moba_selection(q.cpu(), k.cpu(), oracle_cfg(cfg))
+    ref = O.build_csc(sel, hkv, tk)
+    assert torch.equal(index.col_nnz.cpu(), ref["col_nnz"])
+    assert torch.equal(index.col_offsets.cpu(), ref["col_offsets"])
+    assert torch.equal(index.order.cpu(), ref["order"]), "longest-first order differs"
+    assert torch.equal(csc_to_mask(index, s).cpu(), sel)
+    # column membership as a set of (head, row, slot), including slot numbers
+    ic = type(index)(**{f: (getattr(index, f).cpu() if torch.is_tensor(getattr(index, f))
+                            else getattr(index, f)) for f in index.__dataclass_fields__})
+    for bi in range(b):
+        for kv in range(hkv):
+            for blk in range(0, index.num_blocks, max(1, index.num_blocks // 7)):
+                lo = int(ref["col_offsets"][bi, kv, blk])
+                n = int(ref["col_nnz"][bi, kv, blk])
+                want = sorted(zip(ref["head_indices"][bi, kv, lo:lo + n].tolist(),
+                                  ref["row_indices"][bi, kv, lo:lo + n].tolist(),
+                                  ref["slot_of_pair"][bi, kv, lo:lo + n].tolist()))
+                assert column_sets(ic, bi, kv, blk) == want
+
+
+def test_csc_slots_are_dense_and_unique(device):
+    cfg = MoBAConfig(block_size=64, top_k=6)
+    q, k, _ = make_qkv((1, 2048, 2, 64), torch.bfloat16, seed=2, device=device)
+    index = build_csc_fused(q, k, cfg)
+    total = int(index.col_offsets[0, 0, -1])
+    rows = index.row_indices[0, 0, :total].long().cpu()
+    heads = index.head_indices[0, 0, :total].long().cpu()
+    slots = index.slot_of_pair[0, 0, :total].long().cpu()
+    key = (heads * 2048 + rows) * 8 + slots
+    assert key.unique().numel() == total, "a (query, slot) pair appears twice"
+    counts = torch.bincount(heads * 2048 + rows, minlength=2 * 2048)
+    # slot numbers of one query are exactly 0..count-1
+    mx = torch.zeros(2 * 2048, dtype=torch.long).scatter_reduce(0, heads * 2048 + rows, slots,
+                                                                 reduce="amax")
+    assert torch.equal(mx + 1, counts)
+
+
+def test_csc_packed_rows_are_packed_token_indices(device):
+    cfg = MoBAConfig(block_size=16, top_k=3)
+    lens = [80, 48, 64, 20]
+    cu = torch.tensor([0, 80, 128, 192, 212], dtype=torch.int32)
+    q, k, _ = make_qkv((1, 212, 2, 64), torch.bfloat16, seed=5, device=device)
+    index = build_csc_fused(q, k, cfg, cu_seqlens=cu.to(device), max_seqlen=80)
+    sel = O.moba_selection(q.cpu(), k.cpu(), oracle_cfg(cfg), cu_seqlens=cu)
+    assert torch.equal(csc_to_mask(index, 212).cpu(), sel)
+    for r, ln in enumerate(lens):
+        tot = int(index.col_offsets[r, 0, -1])
+        rows = index.row_indices[r, 0, :tot]
+        assert int(rows.min()) >= int(cu[r]) and int(rows.max()) < int(cu[r + 1])
+
+
+def test_csc_unselected_columns_exist(device):
+    cfg = MoBAConfig(block_size=64, top_k=2, always_select_current=False)
+    q, k, _ = make_qkv((1, 1024, 2, 64), torch.bfloat16, device=device)
+    index = build_csc_fused(q, k, cfg)
+    assert bool((index.col_nnz == 0).any())
+    assert int(index.col_offsets[0, 0, -1]) == int(index.col_nnz[0, 0].sum())

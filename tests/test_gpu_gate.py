@@ -1,0 +1,117 @@
+"""Pool and gate on the GPU against the oracle: bitwise kbar, exact ids."""
+
+import pytest
+import torch
+
+from conftest import GATE_SWEEP, SHAPE_SWEEP, make_qkv, oracle_cfg, sweep_cases
+from moba.config import MoBAConfig
+from moba.kernels.gating import gate_select
+from moba.kernels.pooling import pool_blocks
+from oracle import c_oracle
+from oracle import naive as O
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gate(q, k, cfg, cu=None, mx=None):
+    kbar = pool_blocks(k, cfg, cu_seqlens=cu, max_seqlen=mx)
+    return kbar, gate_select(q, kbar, cfg, cu_seqlens=cu, max_seqlen=mx)
+
+
+def check(q, k, cfg, cu=None, mx=None):
+    kbar, idx = run_gate(q, k, cfg, cu, mx)
+    kc = k.cpu()
+    cuc = None if cu is None else cu.cpu()
+    ref_kbar = c_oracle.pool_blocks(kc, cfg.block_size, cuc, mx)
+    got_kbar = kbar.cpu()
+    if cu is not None:  # only rows a sequence owns are defined
+        lens = (cuc[1:] - cuc[:-1]).tolist()
+        for r, ln in enumerate(lens):
+            nb = -(-ln // cfg.block_size)
+            assert torch.equal(got_kbar[r, :, :nb], ref_kbar[r, :, :nb]), f"kbar row {r}"
+    else:
+        assert torch.equal(got_kbar, ref_kbar), "kbar differs from the oracle"
+    ref = c_oracle.gate_select(q.cpu(), ref_kbar, oracle_cfg(cfg), cuc, mx)
+    got = idx.cpu()
+    bad = (got != ref).any(-1)
+    assert not bool(bad.any()), (
+        f"{int(bad.sum())} queries route differently; first {torch.nonzero(bad)[0].tolist()}: "
+        f"got {got[bad][0].tolist()} want {ref[bad][0].tolist()}")
+    return idx
+
+
+@pytest.mark.parametrize("shape,gate", sweep_cases())
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gate_matches_oracle(device, shape, gate, dtype):
+    cfg = MoBAConfig(block_size=gate[0], top_k=gate[1], dtype=dtype)
+    q, k, _ = make_qkv(shape, dtype, device=device)
+    check(q, k, cfg)
+
+
+@pytest.mark.parametrize("gate", [(128, 8), (64, 4)])
+def test_gate_fp32(device, gate):
+    cfg = MoBAConfig(block_size=gate[0], top_k=gate[1], dtype=torch.float32)
+    q, k, _ = make_qkv((1, 2048, 2, 64), torch.float32, device=device)
+    check(q, k, cfg)
+
+
+def test_gate_forced_ties_go_to_block_zero(device):
+    cfg = MoBAConfig(block_size=64, top_k=2)
+    q, k, _ = make_qkv((1, 512, 1, 64), torch.bfloat16, device=device)
+    kbar = pool_blocks(k, cfg)
+    kbar[:] = kbar[:, :, :1, :]
+    idx = gate_select(q, kbar, cfg)
+    assert int(idx[0, 0, 400, 0]) == 0
+    ref = c_oracle.gate_select(q.cpu(), kbar.cpu(), oracle_cfg(cfg))
+    assert torch.equal(idx.cpu(), ref)
+    assert torch.equal(idx, gate_select(q, kbar, cfg)), "gate is not repeatable"
+
+
+@pytest.mark.parametrize("shape,bs,tk", [((1, 512, 2, 64), 128, 12),    # budget > blocks
+                                         ((1, 16384, 1, 64), 32, 64),   # 512 blocks, k=64
+                                         ((1, 1000, 2, 128), 128, 8),   # ragged tail
+                                         ((1, 3000, 2, 64), 96, 5),     # non-pow2 block
+                                         ((1, 2048, 2, 64), 128, 1)])   # own block only
+def test_gate_edge_shapes(device, shape, bs, tk):
+    cfg = MoBAConfig(block_size=bs, top_k=tk)
+    q, k, _ = make_qkv(shape, torch.bfloat16, seed=2, device=device)
+    check(q, k, cfg)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (32, 8, 128), (4, 1, 64)])
+def test_gate_gqa_ranks_per_query_head(device, hq, hkv, d):
+    cfg = MoBAConfig(block_size=64, top_k=4)
+    q, k, _ = make_qkv((1, 2048, hq, d), torch.bfloat16, seed=3, device=device)
+    k = k[:, :, :hkv].contiguous()
+    idx = check(q, k, cfg)
+    # heads sharing a kv head still choose differently
+    assert not torch.equal(idx[0, 0], idx[0, 1])
+
+
+@pytest.mark.parametrize("lens,bs,tk", [([80, 48, 64, 20], 16, 3),
+                                        ([2048, 130, 4000, 777], 128, 8)])
+def test_gate_packed(device, lens, bs, tk):
+    cfg = MoBAConfig(block_size=bs, top_k=tk)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    q, k, _ = make_qkv((1, int(cu[-1]), 2, 64), torch.bfloat16, seed=5, device=device)
+    idx = check(q, k, cfg, cu.to(device), max(lens))
+    # no selected block crosses a sequence boundary (ids are sequence-local)
+    for r, ln in enumerate(lens):
+        lo = int(cu[r])
+        blk = idx[0, :, lo:lo + ln]
+        assert int(blk.max()) < -(-ln // bs)
+
+
+@pytest.mark.parametrize("flags", [dict(always_select_current=False),
+                                   dict(top_k_includes_current=False)])
+def test_gate_nondefault_flags(device, flags):
+    cfg = MoBAConfig(block_size=32, top_k=3, **flags)
+    q, k, _ = make_qkv((1, 1024, 2, 64), torch.bfloat16, seed=6, device=device)
+    check(q, k, cfg)
+
+
+def test_gate_full_size_config2(device):
+    """BASELINE config 2 routing: [1, 65536, 4, 64] bf16, bs128, k8."""
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    q, k, _ = make_qkv((1, 65536, 4, 64), torch.bfloat16, seed=0, device=device)
+    check(q, k, cfg)

@@ -1,0 +1,59 @@
+"""The C ABI library: it loads, exports exactly what include/moba_hip.h
+declares, and rejects bad arguments on the host before touching a GPU."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from moba import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "moba_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moba_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads():
+    lib = _lib.load()
+    assert lib.moba_abi_version() == 1
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), f"{name} missing from {_lib.LIB_PATH}"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_status_strings():
+    lib = _lib.load()
+    assert lib.moba_status_string(0) == b"ok"
+    assert lib.moba_status_string(1) == b"invalid argument"
+
+
+def test_invalid_arguments_fail_on_the_host():
+    lib = _lib.load()
+    rc = lib.moba_pool(None, None, None, 0, 0, 0, 0, 0, 0, 0, 0, None)
+    assert rc == _lib.MOBA_ERR_INVALID
+    assert b"non-positive" in lib.moba_last_error()
+    rc = lib.moba_gate(None, None, None, None, 1, 128, 128, 3, 2, 64, 1, 128, 8, 7, 1, 0,
+                       None, 0, None)
+    assert rc == _lib.MOBA_ERR_INVALID
+    assert b"divisible" in lib.moba_last_error()
+    with pytest.raises(ValueError, match="divisible"):
+        _lib.call("moba_gate", None, None, None, None, 1, 128, 128, 3, 2, 64, 1, 128, 8, 7,
+                  1, 0, None, 0, None)
+
+
+def test_workspace_queries_are_host_only():
+    lib = _lib.load()
+    assert lib.moba_gate_workspace_size(1, 65536, 4) >= 8 * 65536 * 4
+    assert lib.moba_csc_workspace_size(1, 65536, 4, 4, 512, 8) == 4 * 4 * 512
