@@ -1,0 +1,275 @@
+"""MoBA forward + backward throughput on one MI355X.
+
+Metric: fwd & fwd+bwd ms at [1, S, 4, 64] bf16, block_size
+128, top_k 8, S = 64K..512K, plus the fraction of the binding roofline.
+
+A step is one training pass of the hot path on one batch of synthetic input:
+`moba_attention(q, k, v).backward(dO)` -- pool, gate, CSC transpose, attend,
+merge, delta, backward, dQ reduce -- with q, k, v, dO i.i.d. N(0, 1) already
+resident in HBM. The headline workload is S = 524288 (the north star's
+target size); the JSON line also carries the fwd and fwd+bwd sweep over
+S = 64K..512K beside the reference's published H100 numbers.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--seq S]
+       [--no-sweep] [--no-cpu]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "moba-triton_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import torch  # noqa: E402
+
+HEADS, HEAD_DIM, BLOCK, TOPK = 4, 64, 128, 8
+SWEEP = (65536, 131072, 262144, 524288)
+# Reference Triton backend on H100.
+H100_FWD_MS = {65536: 1.492, 131072: 3.942, 262144: 11.609, 524288: 38.164}
+H100_FWDBWD_MS = {65536: 2.658, 131072: 6.181, 262144: 16.076, 524288: 47.046}
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(s, b=1, hq=HEADS, hkv=HEADS, d=HEAD_DIM, k=TOPK, e=2):
+    """Bytes each stage must move at minimum, per call (the per-unit figures
+    of the design's traffic model times the units of one launch)."""
+    n, nkv = b * hq * s, b * hkv * s
+    return {
+        "pool": nkv * d * e,
+        "gate": n * d * e + 4 * n * k,
+        "csc": 20 * n * k,
+        "attend": k * n * d * e + 2 * nkv * d * e + 12 * n * k + n * k * d * e + 8 * n * k,
+        "combine": n * k * d * e + 8 * n * k + n * d * e + 4 * n,
+        "delta": 2 * n * d * e + 4 * n,
+        "bwd": 2 * k * n * d * e + 8 * k * n + 4 * nkv * d * e + k * n * d * e + 12 * n * k,
+        "dq_reduce": k * n * d * e + 4 * n * k + n * d * e,
+    }
+
+
+def make_inputs(s, dev, seed=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    shape = (1, s, HEADS, HEAD_DIM)
+    return [torch.randn(shape, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(4)]
+
+
+def timed(fn, reps, warmup):
+    """Median and min of per-call device time (ms), events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    times.sort()
+    return times[len(times) // 2], times[0]
+
+
+def stage_times(s, dev, reps=5):
+    """Per-stage device time (ms) of one fwd+bwd, each stage timed alone."""
+    from moba.config import MoBAConfig
+    from moba.kernels.gating import gate_select
+    from moba.kernels.moba_bwd import compute_delta, reduce_dq
+    from moba.kernels.moba_fwd import attend_partials, combine_partials
+    from moba.kernels.pooling import pool_blocks
+    from moba.kernels.routing import build_csc_from_indices
+    from moba import _lib
+
+    cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
+    q, k, v, do = make_inputs(s, dev)
+    st = {}
+    kbar = pool_blocks(k, cfg)
+    st["pool"] = timed(lambda: pool_blocks(k, cfg), reps, 1)[0]
+    idx = gate_select(q, kbar, cfg)
+    st["gate"] = timed(lambda: gate_select(q, kbar, cfg), reps, 1)[0]
+    index = build_csc_from_indices(idx, kbar.shape[2], cfg, num_kv_heads=HEADS)
+    st["csc"] = timed(lambda: build_csc_from_indices(idx, kbar.shape[2], cfg,
+                                                     num_kv_heads=HEADS), reps, 1)[0]
+    parts = attend_partials(q, k, v, cfg, index)
+    st["attend"] = timed(lambda: attend_partials(q, k, v, cfg, index, partials=parts),
+                         reps, 1)[0]
+    out, lse = combine_partials(*parts, q.dtype, return_lse=True)
+    st["combine"] = timed(lambda: combine_partials(*parts, q.dtype, return_lse=True),
+                          reps, 1)[0]
+    st["delta"] = timed(lambda: compute_delta(out, do), reps, 1)[0]
+    delta = compute_delta(out, do)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    dq_part = torch.empty((1, HEADS, s, TOPK, HEAD_DIM), device=dev, dtype=q.dtype)
+
+    def bwd():
+        _lib.call("moba_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(do),
+                  _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(index.col_nnz),
+                  _lib.ptr(index.col_offsets), _lib.ptr(index.row_indices),
+                  _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
+                  _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),
+                  None, 1, s, s, HEADS, HEADS, HEAD_DIM, index.num_blocks, BLOCK, TOPK,
+                  index.row_indices.shape[-1], 1, 0, 0, _lib.stream_handle(dev))
+
+    st["bwd"] = timed(bwd, reps, 1)[0]
+    st["dq_reduce"] = timed(lambda: reduce_dq(dq_part, parts[0], q.dtype), reps, 1)[0]
+    return st
+
+
+def sweep(dev, seqs, reps=5):
+    from moba.config import MoBAConfig
+    from moba.kernels.attention import moba_attention
+    from moba.kernels.moba_fwd import moba_forward
+
+    cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
+    rows = []
+    for s in seqs:
+        q, k, v, do = make_inputs(s, dev)
+        fwd = timed(lambda: moba_forward(q, k, v, cfg), reps, 2)[0]
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+        def step():
+            qq.grad = kk.grad = vv.grad = None
+            moba_attention(qq, kk, vv, cfg).backward(do)
+
+        fb = timed(step, reps, 2)[0]
+        rows.append({"seq_len": s, "fwd_ms": round(fwd, 4), "fwd_bwd_ms": round(fb, 4),
+                     "h100_ref_fwd_ms": H100_FWD_MS.get(s),
+                     "h100_ref_fwd_bwd_ms": H100_FWDBWD_MS.get(s),
+                     "speedup_fwd": round(H100_FWD_MS[s] / fwd, 2) if s in H100_FWD_MS else None,
+                     "speedup_fwd_bwd": round(H100_FWDBWD_MS[s] / fb, 2)
+                     if s in H100_FWDBWD_MS else None})
+        del q, k, v, do, qq, kk, vv
+        torch.cuda.empty_cache()
+    return rows
+
+
+def cpu_baseline(s, rows_sample=1024):
+    """The oracle on the host: pool (C), gate (C) for a sample of query rows
+    at full length S, and the float32 sparse-gather attention fwd+bwd (torch
+    autograd) for those rows. Reported as query tokens per second."""
+    from oracle import c_oracle
+    from oracle import naive as O
+    from types import SimpleNamespace
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    ocfg = SimpleNamespace(block_size=BLOCK, top_k=TOPK, always_select_current=True,
+                           top_k_includes_current=True, tie_break_low_index=True)
+    g = torch.Generator().manual_seed(0)
+    shape = (1, s, HEADS, HEAD_DIM)
+    q, k, v, do = (torch.randn(shape, generator=g) for _ in range(4))
+    rows = torch.linspace(0, s - 1, rows_sample).long()
+    t0 = time.perf_counter()
+    kbar = c_oracle.pool_blocks(k, BLOCK)
+    qs = q[:, rows].contiguous()
+    # gate the sampled rows against the full-length representatives
+    n = kbar.shape[2]
+    idx = torch.full((1, HEADS, rows_sample, TOPK), -1, dtype=torch.int32)
+    qs_f = qs.double()
+    kb = kbar.double()
+    for i, t in enumerate(rows.tolist()):
+        own = t // BLOCK
+        take = min(TOPK - 1, own)
+        sc = torch.einsum("hd,hnd->hn", qs_f[0, i], kb[0, :, :own]).float()
+        if take > 0:
+            top = torch.sort(sc, dim=-1, descending=True, stable=True).indices[:, :take]
+            sel = torch.sort(top, dim=-1).values
+            idx[0, :, i, :take] = sel.int()
+        idx[0, :, i, take] = own
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    full_idx = torch.full((1, HEADS, s, TOPK), -1, dtype=torch.int32)
+    full_idx[:, :, rows] = idx
+    out, _ = O.moba_attention_sparse(qg, kg, vg, full_idx, BLOCK, rows=rows)
+    out.backward(do[:, rows])
+    dt = time.perf_counter() - t0
+    return {"value": round(rows_sample / dt, 2), "unit": "query tokens/s (fwd+bwd, 4 heads)",
+            "cores": threads, "kind": "port",
+            "sample": f"{rows_sample} evenly spaced query rows of the S={s} fwd+bwd workload "
+                      f"(C-oracle pool + exact gate for those rows, fp32 sparse-gather "
+                      f"attention fwd+bwd via torch autograd); {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seq", type=int, default=524288)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=2048)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from moba.config import MoBAConfig
+    from moba.kernels.attention import moba_attention
+
+    dev = torch.device("cuda:0")
+    s = args.seq
+    cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
+    q, k, v, do = make_inputs(s, dev)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        qq.grad = kk.grad = vv.grad = None
+        moba_attention(qq, kk, vv, cfg).backward(do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall * 1e3 / args.steps
+    print(f"[bench] S={s} fwd+bwd {ms:.3f} ms/step", file=sys.stderr, flush=True)
+    del qq, kk, vv
+    torch.cuda.empty_cache()
+
+    stages = stage_times(s, dev)
+    ab = algorithmic_bytes(s)
+    dom = max(stages, key=stages.get)
+    achieved = ab[dom] / (stages[dom] * 1e-3) / 1e9
+    stage_rows = {n: {"ms": round(t, 4), "alg_GBps": round(ab[n] / (t * 1e-3) / 1e9, 1)}
+                  for n, t in stages.items()}
+    print(f"[bench] stages {stage_rows}", file=sys.stderr, flush=True)
+    total_alg = sum(ab.values())
+    rows = [] if args.no_sweep else sweep(dev, SWEEP)
+    cpu = None if args.no_cpu else cpu_baseline(s, args.cpu_rows)
+    tokens = s  # query tokens per step (batch 1)
+    line = {
+        "metric": "fwd & fwd+bwd ms at [1,S,4,64] bs128 k8, S=64K..512K; % MFMA/HBM peak",
+        "value": round(tokens / (ms * 1e-3), 1),
+        "unit": "tokens/s (fwd+bwd, S=%d)" % s,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(H100_FWDBWD_MS[s] / ms, 3) if s in H100_FWDBWD_MS else None,
+        "dtype": "bf16", "data": "synthetic (q, k, v, dO i.i.d. N(0,1), seed 0)",
+        "config": {"workload": "moba_fwd_bwd", "batch": 1, "seq_len": s, "heads_q": HEADS,
+                   "heads_kv": HEADS, "head_dim": HEAD_DIM, "block_size": BLOCK,
+                   "top_k": TOPK, "causal": True},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "step_roofline": {"alg_bytes": total_alg,
+                          "alg_GBps": round(total_alg / (ms * 1e-3) / 1e9, 1),
+                          "frac": round(total_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "stages": stage_rows,
+        "sweep": rows,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -10,6 +10,9 @@
 
 namespace moba {
 
+__host__ __device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
 // ---------------------------------------------------------------------------
 // Element types. Storage is raw bits; arithmetic is float.
 // ---------------------------------------------------------------------------
@@ -18,12 +21,12 @@ struct bf16_t { uint16_t bits; };
 struct f16_t { uint16_t bits; };
 
 __host__ __device__ inline float bf16_to_float(uint16_t b) {
-  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  return u2f(static_cast<uint32_t>(b) << 16);
 }
 
 // Round-to-nearest-even float -> bf16 (NaN kept quiet).
 __host__ __device__ inline uint16_t float_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
+  uint32_t u = f2u(f);
   if ((u & 0x7f800000u) == 0x7f800000u) {
     if (u & 0x007fffffu) u |= 0x00400000u;
     return static_cast<uint16_t>(u >> 16);
@@ -32,14 +35,42 @@ __host__ __device__ inline uint16_t float_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-__device__ inline float f16_to_float(uint16_t b) {
-  _Float16 h = __builtin_bit_cast(_Float16, b);
-  return static_cast<float>(h);
+// IEEE binary16 <-> float in integer arithmetic, so the result never depends
+// on the wave's denormal mode (fp16 subnormals are common in pooled means).
+__host__ __device__ inline float f16_to_float(uint16_t h) {
+  const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  const uint32_t m = h & 0x3ffu;
+  if (e == 0) {
+    // m * 2^-24 is a normal float: exact in any denormal mode.
+    const float v = static_cast<float>(m) * 5.9604644775390625e-8f;
+    return u2f(f2u(v) | sign);
+  }
+  if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
 }
 
-__device__ inline uint16_t float_to_f16(float f) {
-  _Float16 h = static_cast<_Float16>(f);  // v_cvt_f16_f32: round to nearest even
-  return __builtin_bit_cast(uint16_t, h);
+// Round-to-nearest-even float -> binary16 (overflow to inf, NaN kept quiet).
+__host__ __device__ inline uint16_t float_to_f16(float f) {
+  const uint32_t u = f2u(f);
+  const uint16_t sign = static_cast<uint16_t>((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00u;            // NaN
+  if (a >= 0x477ff000u) return sign | 0x7c00u;           // >= 65520 -> inf
+  if (a >= 0x38800000u) {                                // normal range
+    uint32_t r = a - 0x38000000u;                        // rebias 127 -> 15
+    r += 0xfffu + ((r >> 13) & 1u);
+    return sign | static_cast<uint16_t>(r >> 13);
+  }
+  if (a < 0x33000000u) return sign;                      // below 2^-25: zero
+  const uint32_t e = a >> 23;                            // subnormal result
+  const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+  const uint32_t shift = 126u - e;                       // in [14, 24]
+  uint32_t q = m >> shift;
+  const uint32_t rem = m & ((1u << shift) - 1u);
+  const uint32_t half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (q & 1u))) ++q;
+  return sign | static_cast<uint16_t>(q);
 }
 
 template <typename T> struct Elem;

@@ -233,6 +233,8 @@ template <> struct MfmaOps<bf16_t> {
   static constexpr float kGapRel = 0.015625f;  // 2^-6 >= 2 bf16 ulps relative
   static constexpr float kGapAbs = 1e-30f;
   static constexpr float kMaxFinite = 3.0e38f;
+  // Largest magnitude the MFMA may flush as a denormal input.
+  static constexpr float kDenorm = 1.2e-38f;
 };
 template <> struct MfmaOps<f16_t> {
   typedef f16x8_t vec;
@@ -242,6 +244,7 @@ template <> struct MfmaOps<f16_t> {
   static constexpr float kGapRel = 0.015625f;
   static constexpr float kGapAbs = 2.0e-7f;    // > 2 fp16 subnormal spacings
   static constexpr float kMaxFinite = 60000.f;  // beyond: fp16 rounds to inf
+  static constexpr float kDenorm = 6.2e-5f;     // fp16 subnormals are below 2^-14
 };
 
 template <typename V>
@@ -383,7 +386,11 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       qn += x * x;
     }
   }
-  const float E = ldexpf(sqrtf(qn) * 1.0001f * kbar_norm[r * h_kv + hk], -14) + 1e-37f;
+  // Accumulation error, plus what flushing denormal operands could drop:
+  // each flushed factor is below kDenorm and its partner below |q| or |kbar|.
+  const float qnorm = sqrtf(qn) * 1.0001f;
+  const float knorm = kbar_norm[r * h_kv + hk];
+  const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
   bool ok = true;
   float cut = -INFINITY;
   if (take > 0 && L > -INFINITY) {

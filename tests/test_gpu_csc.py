@@ -61,7 +61,9 @@ def test_csc_slots_are_dense_and_unique(device):
     # slot numbers of one query are exactly 0..count-1
     mx = torch.zeros(2 * 2048, dtype=torch.long).scatter_reduce(0, heads * 2048 + rows, slots,
                                                                  reduce="amax")
-    assert torch.equal(mx + 1, counts)
+    seen = counts > 0
+    assert bool(seen.any())
+    assert torch.equal((mx + 1)[seen], counts[seen])
 
 
 def test_csc_packed_rows_are_packed_token_indices(device):
