@@ -1,15 +1,468 @@
 // bf16 / fp16 MFMA kernels of the KV-block-major attention (gfx950).
+//
+// Forward (attend_mfma_kernel): one workgroup per (KV block, row * kv head),
+// four waves. The block's K (row-major) and V (transposed, key order
+// permuted per 16-key slice) are staged once in LDS. Each wave then takes
+// groups of 32 column entries and runs, with v_mfma_f32_32x32x16:
+//
+//   S^T[key][q] = K . Q^T        (M = keys, N = queries, K = head_dim)
+//   O^T[d][q]   = V^T . P^T      (M = head_dim, N = queries, K = keys)
+//
+// With the query on the N axis, every lane holds one query's scores, so the
+// row max / sum need one cross-lane step (lane ^ 32) and P^T feeds the second
+// MFMA straight from registers: the C layout of S^T gives lane-half h the
+// keys 16j + 4h + {0..3, 8..11} of K-step j, and V^T is stored with each
+// 16-key slice permuted so those eight keys are contiguous (one 16-byte LDS
+// read per operand). Q rows are gathered from HBM directly into the B
+// operand (each lane one 16-byte chunk of one query row).
+//
+// Semantics: src/moba/kernels/moba_fwd.py:230-425 -- additive tail / causal
+// masks, m = max(q.k * D^-1/2 * log2 e), p = exp2(s - m) rounded to the
+// input dtype for the PV product, l = sum p (float32), partials stored at the
+// query's fixed slot.
 #include "attn_common.h"
 
 namespace moba {
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+  typedef bf16x8_t vec;
+  typedef __bf16 scalar;
+  __device__ static floatx16_t mma(vec a, vec b, floatx16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<f16_t> {
+  typedef f16x8_t vec;
+  typedef _Float16 scalar;
+  __device__ static floatx16_t mma(vec a, vec b, floatx16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename V>
+__device__ inline V ld16(const void* p) {
+  return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));
+}
+
+// Four consecutive elements in one store (8 bytes for 16-bit types).
+template <typename A>
+__device__ inline void store4(A* p, float x0, float x1, float x2, float x3);
+template <>
+__device__ inline void store4<bf16_t>(bf16_t* p, float x0, float x1, float x2, float x3) {
+  uint2 u;
+  u.x = float_to_bf16(x0) | (static_cast<uint32_t>(float_to_bf16(x1)) << 16);
+  u.y = float_to_bf16(x2) | (static_cast<uint32_t>(float_to_bf16(x3)) << 16);
+  *reinterpret_cast<uint2*>(p) = u;
+}
+template <>
+__device__ inline void store4<f16_t>(f16_t* p, float x0, float x1, float x2, float x3) {
+  uint2 u;
+  u.x = float_to_f16(x0) | (static_cast<uint32_t>(float_to_f16(x1)) << 16);
+  u.y = float_to_f16(x2) | (static_cast<uint32_t>(float_to_f16(x3)) << 16);
+  *reinterpret_cast<uint2*>(p) = u;
+}
+template <>
+__device__ inline void store4<float>(float* p, float x0, float x1, float x2, float x3) {
+  *reinterpret_cast<float4*>(p) = make_float4(x0, x1, x2, x3);
+}
+
+// Position of key offset o (within a 16-key slice) in the permuted layout:
+// lane-half h = bit 2 of o owns positions [8h, 8h + 8).
+__device__ inline int perm16(int o) { return ((o >> 2) & 1) * 8 + (o >> 3) * 4 + (o & 3); }
+
+template <typename T, typename A, int D, int BS>
+__global__ void __launch_bounds__(256, (D * BS > 8192) ? 1 : 2)
+attend_mfma_kernel(AttnArgs a) {
+  using M = Mfma<T>;
+  using V8 = typename M::vec;
+  constexpr int KS = D + 8;    // K row stride in LDS (elements): 16-byte aligned, staggered banks
+  constexpr int VS = BS + 8;   // V^T row stride
+  constexpr int KT = BS / 32;  // key tiles of 32
+  constexpr int DT = D / 32;   // head_dim tiles of 32
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[BS * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
+
+  const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
+  if (c.n == 0) return;
+  const int tid = threadIdx.x;
+  const uint16_t* K = static_cast<const uint16_t*>(a.k);
+  const uint16_t* Vg = static_cast<const uint16_t*>(a.v);
+  const uint16_t* Q = static_cast<const uint16_t*>(a.q);
+
+  // Stage K (row-major) and V^T (permuted keys); tail keys are zero.
+  for (int i = tid; i < BS * D / 8; i += 256) {
+    const int key = i / (D / 8);
+    const int d8 = (i % (D / 8)) * 8;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (c.key0 + key < c.key_end) {
+      const int64_t off = ((c.tok0 + key) * a.h_kv + c.hk) * D + d8;
+      kv = *reinterpret_cast<const uint4*>(K + off);
+      vv = *reinterpret_cast<const uint4*>(Vg + off);
+    }
+    *reinterpret_cast<uint4*>(&Ks[key * KS + d8]) = kv;
+    const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
+    const int kp = (key & ~15) + perm16(key & 15);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) Vt[(d8 + u) * VS + kp] = ve[u];
+  }
+  __syncthreads();
+
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;
+  const int col = lane & 31;
+  A* acc_out = static_cast<A*>(a.part_acc);
+
+  for (int32_t g0 = wave * 32; g0 < c.n; g0 += 4 * 32) {
+    const int32_t e = g0 + col;
+    const bool live = e < c.n;
+    const int32_t row = live ? a.row_indices[c.lo + e] : 0;
+    const int32_t head = live ? a.head_indices[c.lo + e] : 0;
+    const int32_t slot = live ? a.slot_of_pair[c.lo + e] : 0;
+
+    // B operand: this lane's query, features 16k + 8h + [0, 8).
+    V8 bq[D / 16];
+    const uint16_t* qrow = Q + q_offset(a, c, row, head);
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k)
+      bq[k] = live ? ld16<V8>(qrow + 16 * k + 8 * h) : V8{};
+
+    floatx16_t s[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      s[kt] = floatx16_t{};
+      const uint16_t* arow = &Ks[(kt * 32 + col) * KS + 8 * h];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) s[kt] = M::mma(ld16<V8>(arow + 16 * k), bq[k], s[kt]);
+    }
+
+    // Masks, row max and sum. s[kt][v] is key 32kt + 8(v/4) + 4h + v%4.
+    // Key / row positions relative to the block start fit in 32 bits.
+    const int key_lim = static_cast<int>(c.key_end - c.key0);
+    const int64_t rrel = static_cast<int64_t>(row) - c.key0;
+    const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
+    const int lim = live ? min(key_lim - 1, row_lim) : -1;  // last visible key
+    float m = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const float x = key <= lim ? s[kt][v] * a.scale_log2 : -INFINITY;
+        s[kt][v] = x;
+        m = fmaxf(m, x);
+      }
+    }
+    m = fmaxf(m, __shfl_xor(m, 32));
+    float l = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const float p = key <= lim ? __builtin_amdgcn_exp2f(s[kt][v] - m) : 0.f;
+        s[kt][v] = p;
+        l += p;
+      }
+    }
+    l += __shfl_xor(l, 32);
+
+    // O^T = V^T . P^T; K-step j takes registers 8(j%2)..+8 of tile j/2.
+    floatx16_t o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = floatx16_t{};
+#pragma unroll
+    for (int j = 0; j < BS / 16; ++j) {
+      V8 bp;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        bp[u] = static_cast<typename M::scalar>(s[j >> 1][8 * (j & 1) + u]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        o[dt] = M::mma(ld16<V8>(&Vt[(dt * 32 + col) * VS + 16 * j + 8 * h]), bp, o[dt]);
+    }
+
+    if (live) {
+      const int64_t dst = part_row(a, c, row, head) * a.slots + slot;
+      if (h == 0) {
+        a.part_m[dst] = m;
+        a.part_l[dst] = l;
+      }
+      // o[dt][v] is feature 32dt + 8(v/4) + 4h + v%4 of this lane's query:
+      // four consecutive features per (dt, v/4).
+      A* base = acc_out + dst * D + 4 * h;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          store4<A>(base + dt * 32 + 8 * q4, o[dt][4 * q4], o[dt][4 * q4 + 1],
+                    o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+    }
+  }
+}
+
+template <typename T, typename A, int D, int BS>
+static int launch_attend(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
+  dim3 grid(static_cast<unsigned>(a.n_blocks), static_cast<unsigned>(n_cols));
+  hipLaunchKernelGGL((attend_mfma_kernel<T, A, D, BS>), grid, dim3(256), 0, st, a);
+  return check_launch("moba_attend (mfma)");
+}
+
+template <typename T, typename A>
+static int attend_dispatch(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
+  if (a.D == 64) {
+    if (a.bs == 128) return launch_attend<T, A, 64, 128>(a, n_cols, st);
+    if (a.bs == 64) return launch_attend<T, A, 64, 64>(a, n_cols, st);
+    if (a.bs == 32) return launch_attend<T, A, 64, 32>(a, n_cols, st);
+  } else if (a.D == 128) {
+    if (a.bs == 128) return launch_attend<T, A, 128, 128>(a, n_cols, st);
+    if (a.bs == 64) return launch_attend<T, A, 128, 64>(a, n_cols, st);
+    if (a.bs == 32) return launch_attend<T, A, 128, 32>(a, n_cols, st);
+  }
+  return MOBA_ERR_UNSUPPORTED;
+}
+
 int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hipStream_t st) {
-  (void)a; (void)dtype; (void)acc_dtype; (void)n_cols; (void)st;
+  if (dtype == MOBA_BF16) {
+    if (acc_dtype == MOBA_BF16) return attend_dispatch<bf16_t, bf16_t>(a, n_cols, st);
+    if (acc_dtype == MOBA_FP32) return attend_dispatch<bf16_t, float>(a, n_cols, st);
+  } else if (dtype == MOBA_FP16) {
+    if (acc_dtype == MOBA_FP16) return attend_dispatch<f16_t, f16_t>(a, n_cols, st);
+    if (acc_dtype == MOBA_FP32) return attend_dispatch<f16_t, float>(a, n_cols, st);
+  }
+  return MOBA_ERR_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// Backward (bwd_mfma_kernel): one workgroup per (KV block, row * kv head),
+// one wave per 32 keys of the block. The workgroup owns its keys' dK / dV
+// for the whole column (registers, stored once: no atomics), and walks the
+// column in groups of 32 entries. Per group, with the group's Q / dO staged
+// in LDS in both orientations:
+//
+//   S[q][key]   = Q . K^T,   dP[q][key] = dO . V^T      (lane <-> key)
+//   P = exp2(S * scale log2e - lse),  dS = P (dP - delta)
+//   dV^T[d][key] += dO^T . P,   dK^T[d][key] += Q^T . dS  (P, dS straight
+//                                                         from registers)
+//   dQ^T[d][q]   = K^T . dS^T over all keys of the block, via dS in LDS
+//
+// and writes one dQ partial per (query, slot) -- summed over the whole block
+// inside the workgroup, so the partial buffer is [.., slots, D], not
+// slots x sub-tiles. Semantics: src/moba/kernels/moba_bwd.py:216-394.
+// ---------------------------------------------------------------------------
+template <typename T, typename A, int D, int BS>
+__global__ void __launch_bounds__(BS * 2, 1)
+bwd_mfma_kernel(AttnArgs a) {
+  using M = Mfma<T>;
+  using V8 = typename M::vec;
+  using Sc = typename M::scalar;
+  constexpr int NW = BS / 32;   // waves: 32 keys each
+  constexpr int NT = NW * 64;   // threads
+  constexpr int DT = D / 32;
+  constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
+  constexpr int KTS = BS + 8;   // row stride of K^T and dS ([*][key])
+  constexpr int QTS = 32 + 8;   // row stride of Q^T / dO^T ([d][q])
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[BS * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[BS * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[32 * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Os[32 * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Qt[D * QTS];
+  __shared__ __attribute__((aligned(16))) uint16_t Ot[D * QTS];
+  __shared__ __attribute__((aligned(16))) uint16_t DS[32 * KTS];
+  __shared__ float s_lse[32], s_delta[32];
+  __shared__ int s_lim[32];
+  __shared__ int64_t s_dst[32];
+
+  const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
+  const int tid = threadIdx.x;
+  const uint16_t* Kg = static_cast<const uint16_t*>(a.k);
+  const uint16_t* Vg = static_cast<const uint16_t*>(a.v);
+  const uint16_t* Qg = static_cast<const uint16_t*>(a.q);
+  const uint16_t* Og = static_cast<const uint16_t*>(a.dout);
+  const int key_lim = static_cast<int>(c.key_end - c.key0);
+
+  for (int i = tid; i < BS * D / 8; i += NT) {
+    const int key = i / (D / 8);
+    const int d8 = (i % (D / 8)) * 8;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (key < key_lim) {
+      const int64_t off = ((c.tok0 + key) * a.h_kv + c.hk) * D + d8;
+      kv = *reinterpret_cast<const uint4*>(Kg + off);
+      vv = *reinterpret_cast<const uint4*>(Vg + off);
+    }
+    *reinterpret_cast<uint4*>(&Ks[key * RS + d8]) = kv;
+    *reinterpret_cast<uint4*>(&Vs[key * RS + d8]) = vv;
+    const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kv);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) Kt[(d8 + u) * KTS + key] = ke[u];
+  }
+
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;
+  const int col = lane & 31;
+  const int mykey = wave * 32 + col;  // the key this lane holds in S / dP / dV / dK
+  floatx16_t dv[DT], dk[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
+  A* dq_out = static_cast<A*>(a.part_acc);
+
+  for (int32_t g0 = 0; g0 < c.n; g0 += 32) {
+    __syncthreads();  // previous group fully consumed (and K / V staged)
+    if (tid < 32) {
+      const int32_t e = g0 + tid;
+      int lim = -1;
+      float lse = 0.f, dl = 0.f;
+      int64_t dst = -1;
+      if (e < c.n) {
+        const int32_t row = a.row_indices[c.lo + e];
+        const int32_t head = a.head_indices[c.lo + e];
+        const int32_t slot = a.slot_of_pair[c.lo + e];
+        const int64_t pr = part_row(a, c, row, head);
+        lse = a.lse[pr];
+        dl = a.delta[pr];
+        dst = pr * a.slots + slot;
+        const int64_t rrel = static_cast<int64_t>(row) - c.key0;
+        const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
+        lim = min(key_lim - 1, row_lim);
+      }
+      s_lim[tid] = lim;
+      s_lse[tid] = lse;
+      s_delta[tid] = dl;
+      s_dst[tid] = dst;
+    }
+    // Q and dO rows of the group: row-major and transposed (q permuted per
+    // 16-slice so each lane-half's eight queries are contiguous).
+    for (int i = tid; i < 32 * D / 8; i += NT) {
+      const int q = i / (D / 8);
+      const int d8 = (i % (D / 8)) * 8;
+      const int32_t e = g0 + q;
+      uint4 qv = make_uint4(0, 0, 0, 0), ov = make_uint4(0, 0, 0, 0);
+      if (e < c.n) {
+        const int32_t row = a.row_indices[c.lo + e];
+        const int32_t head = a.head_indices[c.lo + e];
+        const int64_t off = q_offset(a, c, row, head) + d8;
+        qv = *reinterpret_cast<const uint4*>(Qg + off);
+        ov = *reinterpret_cast<const uint4*>(Og + off);
+      }
+      *reinterpret_cast<uint4*>(&Qs[q * RS + d8]) = qv;
+      *reinterpret_cast<uint4*>(&Os[q * RS + d8]) = ov;
+      const uint16_t* qe = reinterpret_cast<const uint16_t*>(&qv);
+      const uint16_t* oe = reinterpret_cast<const uint16_t*>(&ov);
+      const int qp = (q & ~15) + perm16(q & 15);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        Qt[(d8 + u) * QTS + qp] = qe[u];
+        Ot[(d8 + u) * QTS + qp] = oe[u];
+      }
+    }
+    __syncthreads();
+
+    // S and dP for this wave's 32 keys; lane <-> key, register v <-> query
+    // 8(v/4) + 4h + v%4.
+    floatx16_t sacc = floatx16_t{}, pacc = floatx16_t{};
+    {
+      const uint16_t* qa = &Qs[col * RS + 8 * h];
+      const uint16_t* oa = &Os[col * RS + 8 * h];
+      const uint16_t* kb = &Ks[mykey * RS + 8 * h];
+      const uint16_t* vb = &Vs[mykey * RS + 8 * h];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        sacc = M::mma(ld16<V8>(qa + 16 * k), ld16<V8>(kb + 16 * k), sacc);
+        pacc = M::mma(ld16<V8>(oa + 16 * k), ld16<V8>(vb + 16 * k), pacc);
+      }
+    }
+    V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int q = 8 * (v >> 2) + 4 * h + (v & 3);
+      const bool ok = mykey <= s_lim[q];
+      const float p = ok ? __builtin_amdgcn_exp2f(sacc[v] * a.scale_log2 - s_lse[q]) : 0.f;
+      const float ds = p * (pacc[v] - s_delta[q]);
+      pb[v >> 3][v & 7] = static_cast<Sc>(p);
+      db[v >> 3][v & 7] = static_cast<Sc>(ds);
+      DS[q * KTS + mykey] = __builtin_bit_cast(uint16_t, static_cast<Sc>(ds));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dv[dt] = M::mma(ld16<V8>(&Ot[(dt * 32 + col) * QTS + 16 * j + 8 * h]), pb[j], dv[dt]);
+        dk[dt] = M::mma(ld16<V8>(&Qt[(dt * 32 + col) * QTS + 16 * j + 8 * h]), db[j], dk[dt]);
+      }
+    }
+    __syncthreads();  // dS of every wave visible
+
+    // dQ^T[d][q] over all BS keys; tiles of 32 features spread over waves.
+    for (int dt = wave; dt < DT; dt += NW) {
+      floatx16_t dq = floatx16_t{};
+#pragma unroll
+      for (int j = 0; j < BS / 16; ++j)
+        dq = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
+                    ld16<V8>(&DS[col * KTS + 16 * j + 8 * h]), dq);
+      const int64_t dst = s_dst[col];
+      if (dst >= 0) {
+        A* base = dq_out + dst * D + dt * 32 + 4 * h;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+          store4<A>(base + 8 * q4, dq[4 * q4] * a.scale, dq[4 * q4 + 1] * a.scale,
+                    dq[4 * q4 + 2] * a.scale, dq[4 * q4 + 3] * a.scale);
+      }
+    }
+  }
+
+  // dK, dV of this lane's key: register v is feature 32dt + 8(v/4) + 4h + v%4.
+  if (mykey < key_lim) {
+    const int64_t off = ((c.tok0 + mykey) * a.h_kv + c.hk) * D + 4 * h;
+    T* dK = static_cast<T*>(a.dk) + off;
+    T* dV = static_cast<T*>(a.dv) + off;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        store4<T>(dK + dt * 32 + 8 * q4, dk[dt][4 * q4] * a.scale, dk[dt][4 * q4 + 1] * a.scale,
+                  dk[dt][4 * q4 + 2] * a.scale, dk[dt][4 * q4 + 3] * a.scale);
+        store4<T>(dV + dt * 32 + 8 * q4, dv[dt][4 * q4], dv[dt][4 * q4 + 1],
+                  dv[dt][4 * q4 + 2], dv[dt][4 * q4 + 3]);
+      }
+  }
+}
+
+template <typename T, typename A, int D, int BS>
+static int launch_bwd(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
+  dim3 grid(static_cast<unsigned>(a.n_blocks), static_cast<unsigned>(n_cols));
+  hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS>), grid, dim3(BS * 2), 0, st, a);
+  return check_launch("moba_bwd (mfma)");
+}
+
+template <typename T, typename A>
+static int bwd_dispatch(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
+  if (a.D == 64) {
+    if (a.bs == 128) return launch_bwd<T, A, 64, 128>(a, n_cols, st);
+    if (a.bs == 64) return launch_bwd<T, A, 64, 64>(a, n_cols, st);
+    if (a.bs == 32) return launch_bwd<T, A, 64, 32>(a, n_cols, st);
+  } else if (a.D == 128) {
+    if (a.bs == 128) return launch_bwd<T, A, 128, 128>(a, n_cols, st);
+    if (a.bs == 64) return launch_bwd<T, A, 128, 64>(a, n_cols, st);
+    if (a.bs == 32) return launch_bwd<T, A, 128, 32>(a, n_cols, st);
+  }
   return MOBA_ERR_UNSUPPORTED;
 }
 
 int bwd_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hipStream_t st) {
-  (void)a; (void)dtype; (void)acc_dtype; (void)n_cols; (void)st;
+  if (dtype == MOBA_BF16) {
+    if (acc_dtype == MOBA_BF16) return bwd_dispatch<bf16_t, bf16_t>(a, n_cols, st);
+    if (acc_dtype == MOBA_FP32) return bwd_dispatch<bf16_t, float>(a, n_cols, st);
+  } else if (dtype == MOBA_FP16) {
+    if (acc_dtype == MOBA_FP16) return bwd_dispatch<f16_t, f16_t>(a, n_cols, st);
+    if (acc_dtype == MOBA_FP32) return bwd_dispatch<f16_t, float>(a, n_cols, st);
+  }
   return MOBA_ERR_UNSUPPORTED;
 }
 

@@ -321,32 +321,71 @@ bwd_dq_simple_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Row-wise passes: combine, delta, dq reduce.
 // ---------------------------------------------------------------------------
+// Eight consecutive elements as floats / from floats (16-byte accesses for
+// 16-bit types).
+template <typename A>
+__device__ inline void load8(const A* p, float (&x)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint16_t* e = reinterpret_cast<const uint16_t*>(&u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = Elem<A>::load(reinterpret_cast<const A*>(e), i);
+}
+template <>
+__device__ inline void load8<float>(const float* p, float (&x)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+template <typename A>
+__device__ inline void store8(A* p, const float (&x)[8]) {
+  uint4 u;
+  uint16_t* e = reinterpret_cast<uint16_t*>(&u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) Elem<A>::store(reinterpret_cast<A*>(e), i, x[i]);
+  *reinterpret_cast<uint4*>(p) = u;
+}
+template <>
+__device__ inline void store8<float>(float* p, const float (&x)[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
+}
+
+// One lane per (query, 8 features). Two passes over the slots, as in the
+// reference merge: the global max, then the rescaled sums.
 template <typename A, typename O>
 __global__ void __launch_bounds__(256)
 combine_kernel(const float* __restrict__ part_m, const float* __restrict__ part_l,
                const A* __restrict__ part_acc, O* __restrict__ out, float* __restrict__ lse,
                int64_t n_rows, int64_t S, int64_t h_q, int64_t D, int64_t slots) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t row = gid / D;     // head-major (b * Hq + h) * S + t
-  const int64_t d = gid % D;
+  const int64_t per_row = D / 8;
+  const int64_t row = gid / per_row;     // head-major (b * Hq + h) * S + t
+  const int64_t d0 = (gid % per_row) * 8;
   if (row >= n_rows) return;
   const float* m = part_m + row * slots;
   const float* l = part_l + row * slots;
   float m_g = -INFINITY;
   for (int64_t j = 0; j < slots; ++j) m_g = fmaxf(m_g, m[j]);
-  float ls = 0.f, acc = 0.f;
+  float ls = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < slots; ++j) {
     const float mi = m[j];
     if (mi > -INFINITY) {
       const float w = exp2f(mi - m_g);
       ls += l[j] * w;
-      acc += Elem<A>::load(part_acc, (row * slots + j) * D + d) * w;
+      float x[8];
+      load8<A>(part_acc + (row * slots + j) * D + d0, x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += x[i] * w;
     }
   }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = acc[i] / ls;  // l == 0 (index bug) -> NaN, loudly
   const int64_t bh = row / S, t = row % S;
   const int64_t b = bh / h_q, h = bh % h_q;
-  Elem<O>::store(out, ((b * S + t) * h_q + h) * D + d, acc / ls);
-  if (lse && d == 0) lse[row] = m_g + log2f(ls);
+  store8<O>(out + ((b * S + t) * h_q + h) * D + d0, acc);
+  if (lse && d0 == 0) lse[row] = m_g + log2f(ls);
 }
 
 template <typename T>
@@ -367,22 +406,29 @@ delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, float* __restr
   if (lane == 0) delta[row] = acc;
 }
 
+// One lane per (query, 8 features); a slot counts only if the forward wrote
+// it (part_m > -inf), so unwritten dq partials are never read.
 template <typename A, typename O>
 __global__ void __launch_bounds__(256)
 dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m,
                  O* __restrict__ dq, int64_t n_rows, int64_t S, int64_t h_q, int64_t D,
                  int64_t slots) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t row = gid / D;
-  const int64_t d = gid % D;
+  const int64_t per_row = D / 8;
+  const int64_t row = gid / per_row;
+  const int64_t d0 = (gid % per_row) * 8;
   if (row >= n_rows) return;
-  float acc = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < slots; ++j)
-    if (part_m[row * slots + j] > -INFINITY)
-      acc += Elem<A>::load(dq_part, (row * slots + j) * D + d);
+    if (part_m[row * slots + j] > -INFINITY) {
+      float x[8];
+      load8<A>(dq_part + (row * slots + j) * D + d0, x);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += x[i];
+    }
   const int64_t bh = row / S, t = row % S;
   const int64_t b = bh / h_q, h = bh % h_q;
-  Elem<O>::store(dq, ((b * S + t) * h_q + h) * D + d, acc);
+  store8<O>(dq + ((b * S + t) * h_q + h) * D + d0, acc);
 }
 
 __global__ void __launch_bounds__(256)
@@ -505,8 +551,9 @@ extern "C" int moba_combine(const float* part_m, const float* part_l, const void
   if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0 || slots <= 0)
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
   if (!part_m || !part_l || !part_acc || !out) return fail(MOBA_ERR_INVALID, "null pointer");
+  if (head_dim % 8) return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
   const int64_t n_rows = batch * h_q * seq_len;
-  dim3 grid(static_cast<unsigned>(cdiv(n_rows * head_dim, 256)));
+  dim3 grid(static_cast<unsigned>(cdiv(n_rows * (head_dim / 8), 256)));
   return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
     return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
       hipLaunchKernelGGL((combine_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
@@ -591,8 +638,9 @@ extern "C" int moba_dq_reduce(const void* dq_part, const float* part_m, void* dq
   if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0 || slots <= 0)
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
   if (!dq_part || !part_m || !dq) return fail(MOBA_ERR_INVALID, "null pointer");
+  if (head_dim % 8) return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
   const int64_t n_rows = batch * h_q * seq_len;
-  dim3 grid(static_cast<unsigned>(cdiv(n_rows * head_dim, 256)));
+  dim3 grid(static_cast<unsigned>(cdiv(n_rows * (head_dim / 8), 256)));
   return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
     return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
       hipLaunchKernelGGL((dq_reduce_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),

@@ -57,6 +57,74 @@ count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __
   }
 }
 
+// Workgroup-aggregated variant: 256 queries of one (row, query head) per
+// workgroup, one lane per query. Selections are first counted in an LDS
+// histogram over the blocks this tile can see, so the global counter of each
+// block is touched once per workgroup -- the own block, which every query of
+// a block selects, would otherwise take 128 serialised global atomics. The
+// scatter pass reserves each block's range with one global atomic and hands
+// out positions from LDS.
+constexpr int kTileQ = 256;
+constexpr int kMaxBins = 16384;
+
+template <bool kScatter>
+__global__ void __launch_bounds__(kTileQ)
+tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
+                             const int32_t* __restrict__ cu, int64_t S, int64_t h_q,
+                             int64_t h_kv, int64_t n_blocks, int64_t bs, int slots,
+                             int64_t cap, int32_t* __restrict__ col_nnz_or_cursor,
+                             const int32_t* __restrict__ col_offsets,
+                             int32_t* __restrict__ row_indices,
+                             int32_t* __restrict__ head_indices,
+                             int32_t* __restrict__ slot_of_pair) {
+  __shared__ int32_t bins[kMaxBins];
+  const int64_t rh = blockIdx.y;
+  const int64_t r = rh / h_q;
+  const int64_t hq = rh % h_q;
+  const int64_t hk = hq / (h_q / h_kv);
+  const bool packed = cu != nullptr;
+  const SeqSpan sp = seq_span(cu, r, S);
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTileQ;
+  if (t0 >= sp.len) return;
+  const int64_t t_last = (t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len) - 1;
+  const int64_t nv = t_last / bs + 1;  // blocks any query here can select
+  const int nvis = static_cast<int>(nv < n_blocks ? nv : n_blocks);
+  for (int b = threadIdx.x; b < nvis; b += kTileQ) bins[b] = 0;
+  __syncthreads();
+  const int64_t t = t0 + threadIdx.x;
+  const bool live = t < sp.len;
+  const int64_t tok = sp.bos + t;
+  const int64_t qid = packed ? hq * S + tok : (r * h_q + hq) * S + t;
+  if (live)
+    for (int j = 0; j < slots; ++j) {
+      const int32_t blk = block_idx[qid * slots + j];
+      if (blk >= 0) atomicAdd(&bins[blk], 1);
+    }
+  __syncthreads();
+  const int64_t colbase = (r * h_kv + hk) * n_blocks;
+  for (int b = threadIdx.x; b < nvis; b += kTileQ) {
+    const int32_t n = bins[b];
+    if (n > 0) {
+      const int32_t base = atomicAdd(&col_nnz_or_cursor[colbase + b], n);
+      if (kScatter) bins[b] = base;
+    }
+  }
+  if (!kScatter) return;
+  __syncthreads();
+  if (!live) return;
+  const int64_t obase = (r * h_kv + hk) * (n_blocks + 1);
+  const int64_t ibase = (r * h_kv + hk) * cap;
+  for (int j = 0; j < slots; ++j) {
+    const int32_t blk = block_idx[qid * slots + j];
+    if (blk < 0) continue;
+    const int32_t within = atomicAdd(&bins[blk], 1);
+    const int64_t dst = ibase + col_offsets[obase + blk] + within;
+    row_indices[dst] = static_cast<int32_t>(packed ? tok : t);
+    head_indices[dst] = static_cast<int32_t>(hq);
+    slot_of_pair[dst] = j;
+  }
+}
+
 // Exclusive scan of one (row, kv head)'s counts; one workgroup each.
 __global__ void __launch_bounds__(1024)
 scan_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ col_offsets,
@@ -148,21 +216,39 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   const unsigned fill_blocks = static_cast<unsigned>(cdiv(ncols, 256) < 4096 ? cdiv(ncols, 256) : 4096);
   hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, col_nnz, ncols, 0);
   hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, cursor, ncols, 0);
+  // A lower bound on the block size: cdiv(rows, n_blocks) <= block_size, so
+  // t / bs_eff never under-counts the blocks a query can see.
+  const bool tiled = n_blocks <= kMaxBins;
+  const int64_t bs_eff = cdiv(g.rows_per_seq, n_blocks);
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq * slots, 256)),
             static_cast<unsigned>(batch * h_q));
-  hipLaunchKernelGGL(count_or_scatter_kernel<false>, grid, dim3(256), 0, s, block_idx,
-                     cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
-                     static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
-                     nullptr);
+  dim3 tgrid(static_cast<unsigned>(cdiv(g.rows_per_seq, kTileQ)),
+             static_cast<unsigned>(batch * h_q));
+  if (tiled)
+    hipLaunchKernelGGL(tile_count_or_scatter_kernel<false>, tgrid, dim3(kTileQ), 0, s,
+                       block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
+                       static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
+                       nullptr);
+  else
+    hipLaunchKernelGGL(count_or_scatter_kernel<false>, grid, dim3(256), 0, s, block_idx,
+                       cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
+                       static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
+                       nullptr);
   hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024), 0, s,
                      col_nnz, col_offsets, n_blocks);
   hipLaunchKernelGGL(order_kernel,
                      dim3(static_cast<unsigned>(cdiv(n_blocks, 256)),
                           static_cast<unsigned>(batch * h_kv)),
                      dim3(256), 0, s, col_nnz, order, n_blocks);
-  hipLaunchKernelGGL(count_or_scatter_kernel<true>, grid, dim3(256), 0, s, block_idx,
-                     cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
-                     static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
-                     head_indices, slot_of_pair);
+  if (tiled)
+    hipLaunchKernelGGL(tile_count_or_scatter_kernel<true>, tgrid, dim3(kTileQ), 0, s,
+                       block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
+                       static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
+                       head_indices, slot_of_pair);
+  else
+    hipLaunchKernelGGL(count_or_scatter_kernel<true>, grid, dim3(256), 0, s, block_idx,
+                       cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
+                       static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
+                       head_indices, slot_of_pair);
   return check_launch("moba_csc_build");
 }

@@ -222,6 +222,63 @@ gate_exact_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 }
 
 // ---------------------------------------------------------------------------
+// Queue kernel: one wave per queued query. Lanes split the candidates, keep
+// exact top-T lists, and merge them with a butterfly over the wave.
+// ---------------------------------------------------------------------------
+template <typename T, int TMAX>
+__global__ void __launch_bounds__(256)
+gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
+                  int32_t* __restrict__ out, const int32_t* __restrict__ cu,
+                  int64_t S, int64_t rows_per_seq, int64_t h_q, int64_t h_kv,
+                  int D, int64_t n_blocks, int bs, int take, int cur, int slots,
+                  const int64_t* __restrict__ queue, const int* __restrict__ queue_len) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (blockDim.x / 64);
+  const int64_t total = *queue_len;
+  const bool packed = cu != nullptr;
+  for (int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
+       item < total; item += n_waves) {
+    const int64_t code = queue[item];  // (r * h_q + hq) * rows_per_seq + t
+    const int64_t t = code % rows_per_seq;
+    const int64_t rh = code / rows_per_seq;
+    const int64_t r = rh / h_q, hq = rh % h_q;
+    const SeqSpan sp = seq_span(cu, r, S);
+    const int64_t tok = sp.bos + t;
+    const T* qrow = q + (tok * h_q + hq) * D;
+    const T* kb = kbar + (r * h_kv + hq / (h_q / h_kv)) * n_blocks * D;
+    const int own = static_cast<int>(t / bs);
+    float val[TMAX];
+    int idx[TMAX];
+#pragma unroll
+    for (int p = 0; p < TMAX; ++p) { val[p] = -INFINITY; idx[p] = 0x7fffffff; }
+    for (int j = lane; j < own; j += 64) {
+      const float s = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
+      if (ranks_before(s, j, val[take - 1], idx[take - 1])) insert_exact<TMAX>(val, idx, s, j);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      float pv[TMAX];
+      int pi[TMAX];
+#pragma unroll
+      for (int p = 0; p < TMAX; ++p) {
+        pv[p] = __shfl_xor(val[p], off);
+        pi[p] = __shfl_xor(idx[p], off);
+      }
+#pragma unroll
+      for (int p = 0; p < TMAX; ++p)
+        if (pv[p] > -INFINITY) insert_exact<TMAX>(val, idx, pv[p], pi[p]);
+    }
+    if (lane == 0) {
+      int n_sel = 0;
+#pragma unroll
+      for (int p = 0; p < TMAX; ++p)
+        if (p < take && val[p] > -INFINITY) n_sel = p + 1;
+      emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
+                        out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA kernel (bf16 / fp16).
 // ---------------------------------------------------------------------------
 template <typename T> struct MfmaOps;
@@ -230,7 +287,9 @@ template <> struct MfmaOps<bf16_t> {
   __device__ static floatx16_t mfma(vec a, vec b, floatx16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static constexpr float kGapRel = 0.015625f;  // 2^-6 >= 2 bf16 ulps relative
+  // Two values more than one bf16 ulp apart (<= 2^-7 relative) can never
+  // round to the same bf16 value; 1% slack on top.
+  static constexpr float kGapRel = 0.0078125f * 1.01f;
   static constexpr float kGapAbs = 1e-30f;
   static constexpr float kMaxFinite = 3.0e38f;
   // Largest magnitude the MFMA may flush as a denormal input.
@@ -241,7 +300,7 @@ template <> struct MfmaOps<f16_t> {
   __device__ static floatx16_t mfma(vec a, vec b, floatx16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static constexpr float kGapRel = 0.015625f;
+  static constexpr float kGapRel = 0.0078125f * 1.01f;  // covers fp16's 2^-10 ulps
   static constexpr float kGapAbs = 2.0e-7f;    // > 2 fp16 subnormal spacings
   static constexpr float kMaxFinite = 60000.f;  // beyond: fp16 rounds to inf
   static constexpr float kDenorm = 6.2e-5f;     // fp16 subnormals are below 2^-14
@@ -309,19 +368,27 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     float thr = -INFINITY;
     int cnt = 0;
     const int n_chunks = (horizon + 31) / 32;
+    // A operands of the next chunk are fetched while this one is scored.
+    // Rows past the horizon are clamped to a valid row; their scores are
+    // masked below (every such block is >= own for every query here).
+    V acur[KSTEPS], anext[KSTEPS];
+    {
+      const T* ap = kb + static_cast<int64_t>(min(col, horizon - 1)) * D + 8 * half;
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) acur[c] = load_vec16<V>(ap + 16 * c);
+    }
     for (int ch = 0; ch < n_chunks; ++ch) {
       const int blk0 = ch * 32;
-      const int arow = blk0 + col;  // A row this lane supplies
-      floatx16_t acc = {};
-      if (arow < horizon) {
-        const T* ap = kb + static_cast<int64_t>(arow) * D + 8 * half;
+      if (ch + 1 < n_chunks) {
+        const T* ap = kb + static_cast<int64_t>(min(blk0 + 32 + col, horizon - 1)) * D + 8 * half;
 #pragma unroll
-        for (int c = 0; c < KSTEPS; ++c)
-          acc = Ops::mfma(load_vec16<V>(ap + 16 * c), bq[c], acc);
-      } else {
-#pragma unroll
-        for (int c = 0; c < KSTEPS; ++c) acc = Ops::mfma(V{}, bq[c], acc);
+        for (int c = 0; c < KSTEPS; ++c) anext[c] = load_vec16<V>(ap + 16 * c);
       }
+      floatx16_t acc = {};
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) acc = Ops::mfma(acur[c], bq[c], acc);
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) acur[c] = anext[c];
       // acc[v] is the score of block blk0 + 8*(v/4) + 4*half + v%4.
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -519,15 +586,28 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   int rc = check_launch("moba_gate (prep)");
   if (rc) return rc;
   if (g.head_dim == 64) {
-    rc = take <= 8 ? launch_mfma<T, 64, 8>(q, kbar, out, cu, g, take, cur, ws, st)
-                   : launch_mfma<T, 64, 16>(q, kbar, out, cu, g, take, cur, ws, st);
+    rc = take <= 8 ? launch_mfma<T, 64, 12>(q, kbar, out, cu, g, take, cur, ws, st)
+                   : launch_mfma<T, 64, 20>(q, kbar, out, cu, g, take, cur, ws, st);
   } else {
-    rc = take <= 8 ? launch_mfma<T, 128, 8>(q, kbar, out, cu, g, take, cur, ws, st)
-                   : launch_mfma<T, 128, 16>(q, kbar, out, cu, g, take, cur, ws, st);
+    rc = take <= 8 ? launch_mfma<T, 128, 12>(q, kbar, out, cu, g, take, cur, ws, st)
+                   : launch_mfma<T, 128, 20>(q, kbar, out, cu, g, take, cur, ws, st);
   }
   if (rc) return rc;
-  // Queries whose approximate evidence was insufficient: exact rescoring.
-  return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, ws.queue, ws.counter, st);
+  // Queries whose approximate evidence was insufficient: exact rescoring,
+  // one wave per query.
+  if (take <= 8)
+    hipLaunchKernelGGL((gate_queue_kernel<T, 8>), dim3(1024), dim3(256), 0, st,
+                       static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
+                       g.seq_len, g.rows_per_seq, g.h_q, g.h_kv, static_cast<int>(g.head_dim),
+                       g.n_blocks, static_cast<int>(g.block_size), take, cur,
+                       static_cast<int>(g.slots), ws.queue, ws.counter);
+  else
+    hipLaunchKernelGGL((gate_queue_kernel<T, 16>), dim3(1024), dim3(256), 0, st,
+                       static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
+                       g.seq_len, g.rows_per_seq, g.h_q, g.h_kv, static_cast<int>(g.head_dim),
+                       g.n_blocks, static_cast<int>(g.block_size), take, cur,
+                       static_cast<int>(g.slots), ws.queue, ws.counter);
+  return check_launch("moba_gate (queue)");
   }
 }
 
