@@ -313,56 +313,79 @@ bwd_mfma_kernel(AttnArgs a) {
   for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
   A* dq_out = static_cast<A*>(a.part_acc);
 
-  for (int32_t g0 = 0; g0 < c.n; g0 += 32) {
-    __syncthreads();  // previous group fully consumed (and K / V staged)
+  // The next group's entry metadata and Q / dO rows are fetched into
+  // registers while the current group is computed, then written to LDS.
+  constexpr int CH = (32 * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per tensor
+  uint4 pq[CH], po[CH];
+  int p_lim = -1;
+  float p_lse = 0.f, p_dl = 0.f;
+  int64_t p_dst = -1;
+  auto fetch = [&](int32_t g0) {
     if (tid < 32) {
       const int32_t e = g0 + tid;
-      int lim = -1;
-      float lse = 0.f, dl = 0.f;
-      int64_t dst = -1;
+      p_lim = -1; p_lse = 0.f; p_dl = 0.f; p_dst = -1;
       if (e < c.n) {
         const int32_t row = a.row_indices[c.lo + e];
         const int32_t head = a.head_indices[c.lo + e];
         const int32_t slot = a.slot_of_pair[c.lo + e];
         const int64_t pr = part_row(a, c, row, head);
-        lse = a.lse[pr];
-        dl = a.delta[pr];
-        dst = pr * a.slots + slot;
+        p_lse = a.lse[pr];
+        p_dl = a.delta[pr];
+        p_dst = pr * a.slots + slot;
         const int64_t rrel = static_cast<int64_t>(row) - c.key0;
         const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
-        lim = min(key_lim - 1, row_lim);
+        p_lim = min(key_lim - 1, row_lim);
       }
-      s_lim[tid] = lim;
-      s_lse[tid] = lse;
-      s_delta[tid] = dl;
-      s_dst[tid] = dst;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int i = tid + u * NT;
+      pq[u] = make_uint4(0, 0, 0, 0);
+      po[u] = make_uint4(0, 0, 0, 0);
+      if (i < 32 * D / 8) {
+        const int32_t e = g0 + i / (D / 8);
+        if (e < c.n) {
+          const int32_t row = a.row_indices[c.lo + e];
+          const int32_t head = a.head_indices[c.lo + e];
+          const int64_t off = q_offset(a, c, row, head) + (i % (D / 8)) * 8;
+          pq[u] = *reinterpret_cast<const uint4*>(Qg + off);
+          po[u] = *reinterpret_cast<const uint4*>(Og + off);
+        }
+      }
+    }
+  };
+  fetch(0);
+
+  for (int32_t g0 = 0; g0 < c.n; g0 += 32) {
+    __syncthreads();  // previous group fully consumed (and K / V staged)
+    if (tid < 32) {
+      s_lim[tid] = p_lim;
+      s_lse[tid] = p_lse;
+      s_delta[tid] = p_dl;
+      s_dst[tid] = p_dst;
     }
     // Q and dO rows of the group: row-major and transposed (q permuted per
     // 16-slice so each lane-half's eight queries are contiguous).
-    for (int i = tid; i < 32 * D / 8; i += NT) {
-      const int q = i / (D / 8);
-      const int d8 = (i % (D / 8)) * 8;
-      const int32_t e = g0 + q;
-      uint4 qv = make_uint4(0, 0, 0, 0), ov = make_uint4(0, 0, 0, 0);
-      if (e < c.n) {
-        const int32_t row = a.row_indices[c.lo + e];
-        const int32_t head = a.head_indices[c.lo + e];
-        const int64_t off = q_offset(a, c, row, head) + d8;
-        qv = *reinterpret_cast<const uint4*>(Qg + off);
-        ov = *reinterpret_cast<const uint4*>(Og + off);
-      }
-      *reinterpret_cast<uint4*>(&Qs[q * RS + d8]) = qv;
-      *reinterpret_cast<uint4*>(&Os[q * RS + d8]) = ov;
-      const uint16_t* qe = reinterpret_cast<const uint16_t*>(&qv);
-      const uint16_t* oe = reinterpret_cast<const uint16_t*>(&ov);
-      const int qp = (q & ~15) + perm16(q & 15);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        Qt[(d8 + u) * QTS + qp] = qe[u];
-        Ot[(d8 + u) * QTS + qp] = oe[u];
+    for (int u = 0; u < CH; ++u) {
+      const int i = tid + u * NT;
+      if (i < 32 * D / 8) {
+        const int q = i / (D / 8);
+        const int d8 = (i % (D / 8)) * 8;
+        *reinterpret_cast<uint4*>(&Qs[q * RS + d8]) = pq[u];
+        *reinterpret_cast<uint4*>(&Os[q * RS + d8]) = po[u];
+        const uint16_t* qe = reinterpret_cast<const uint16_t*>(&pq[u]);
+        const uint16_t* oe = reinterpret_cast<const uint16_t*>(&po[u]);
+        const int qp = (q & ~15) + perm16(q & 15);
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          Qt[(d8 + w) * QTS + qp] = qe[w];
+          Ot[(d8 + w) * QTS + qp] = oe[w];
+        }
       }
     }
     __syncthreads();
+    if (g0 + 32 < c.n) fetch(g0 + 32);
 
     // S and dP for this wave's 32 keys; lane <-> key, register v <-> query
     // 8(v/4) + 4h + v%4.

@@ -126,6 +126,22 @@ __device__ inline void insert_exact(float (&val)[M], int (&idx)[M], float s, int
   }
 }
 
+// Branch-free insertion into a list sorted by value only (approximate scores;
+// ties among them are settled later by the exact rescoring).
+template <int M>
+__device__ inline void insert_approx(float (&val)[M], int (&idx)[M], float s, int j) {
+#pragma unroll
+  for (int p = 0; p < M; ++p) {
+    const bool gt = s > val[p];
+    const float nv = gt ? s : val[p];
+    const int ni = gt ? j : idx[p];
+    s = gt ? val[p] : s;
+    j = gt ? idx[p] : j;
+    val[p] = nv;
+    idx[p] = ni;
+  }
+}
+
 // Emits own block + selected ids ascending, -1 padded, into `out[0..slots)`.
 template <int M>
 __device__ inline void emit_sorted(int (&sel)[M], int n_sel, int own, bool cur,
@@ -312,7 +328,7 @@ __device__ inline V load_vec16(const void* p) {
   return __builtin_bit_cast(V, u);
 }
 
-template <typename T, int D, int M, int CAP, int WAVES>
+template <typename T, int D, int M, int K, int CAP, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64)
 gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                  int32_t* __restrict__ out, const int32_t* __restrict__ cu,
@@ -323,11 +339,16 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   using Ops = MfmaOps<T>;
   using V = typename Ops::vec;
   constexpr int KSTEPS = D / 16;
+  constexpr int KROW = D + 8;                      // staged kbar row stride (elements)
+  constexpr int NT = WAVES * 64;
+  constexpr int KCH = (32 * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per stage
   __shared__ float s_val[WAVES][CAP][64];
-  __shared__ int s_idx[WAVES][CAP][64];
+  __shared__ uint16_t s_idx[WAVES][CAP][64];
+  __shared__ __attribute__((aligned(16))) uint16_t s_kb[2][32 * KROW];
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int half = lane >> 5;
   const int col = lane & 31;
   const bool packed = cu != nullptr;
@@ -340,95 +361,184 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Tiles are numbered from the end so the longest ones start first.
   const int64_t n_tiles = (rows_per_seq + 32 * WAVES - 1) / (32 * WAVES);
   const int64_t tile = n_tiles - 1 - blockIdx.x;
-  const int64_t t0 = tile * 32 * WAVES + wave * 32;
-  if (t0 >= sp.len) return;
-  const int64_t t = t0 + col;
+  const int64_t twg = tile * 32 * WAVES;
+  if (twg >= sp.len) return;  // uniform over the workgroup
+  const int64_t t = twg + wave * 32 + col;
   const bool live = t < sp.len;
   const int own = live ? static_cast<int>(t / bs) : 0;
-  const int64_t last_t = (t0 + 31 < sp.len ? t0 + 31 : sp.len - 1);
-  const int horizon = static_cast<int>(last_t / bs);  // candidates are < own
+  // Blocks any query of the workgroup may rank: [0, hz).
+  const int64_t last_wg = (twg + 32 * WAVES - 1 < sp.len ? twg + 32 * WAVES - 1 : sp.len - 1);
+  const int hz = static_cast<int>(last_wg / bs);
   const T* kb = kbar + (r * h_kv + hk) * n_blocks * D;
-  const int64_t tok = sp.bos + (live ? t : t0);
+  const int64_t tok = sp.bos + (live ? t : 0);
   const T* qrow = q + (tok * h_q + hq) * D;
 
+  // B operand: this lane's query, features 16c + 8*half + [0, 8). The two
+  // lanes of a query hold complementary halves of it.
+  V bq[KSTEPS];
+#pragma unroll
+  for (int c = 0; c < KSTEPS; ++c) {
+    if (live) bq[c] = load_vec16<V>(qrow + 16 * c + 8 * half);
+    else bq[c] = V{};
+  }
+  // Error band of this query: E >= |approx - exact| for every candidate.
+  float qn = 0.f;
+#pragma unroll
+  for (int c = 0; c < KSTEPS; ++c)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = static_cast<float>(bq[c][i]);
+      qn += x * x;
+    }
+  qn += __shfl_xor(qn, 32);
+  // Accumulation error, plus what flushing denormal operands could drop:
+  // each flushed factor is below kDenorm and its partner below |q| or |kbar|.
+  const float qnorm = sqrtf(qn) * 1.0001f;
+  const float knorm = kbar_norm[r * h_kv + hk];
+  const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
+
+  const int n_chunks = (take > 0 && hz > 0) ? (hz + 31) / 32 : 0;
+  // kbar chunks of 32 rows are staged in LDS by the whole workgroup. Rows
+  // past the horizon are clamped to a valid row; their scores are masked
+  // (every such block is >= own for every query here).
+  uint4 kreg[KCH];
+  auto kload = [&](int ch) {
+#pragma unroll
+    for (int u = 0; u < KCH; ++u) {
+      const int i = tid + u * NT;
+      if (i < 32 * D / 8) {
+        const int blk = min(ch * 32 + i / (D / 8), hz - 1);
+        kreg[u] = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(blk) * D +
+                                                 (i % (D / 8)) * 8);
+      }
+    }
+  };
+  auto kstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < KCH; ++u) {
+      const int i = tid + u * NT;
+      if (i < 32 * D / 8)
+        *reinterpret_cast<uint4*>(&s_kb[buf][(i / (D / 8)) * KROW + (i % (D / 8)) * 8]) =
+            kreg[u];
+    }
+  };
+  auto score_chunk = [&](int buf) {
+    const uint16_t* arow = &s_kb[buf][col * KROW + 8 * half];
+    floatx16_t acc = {};
+#pragma unroll
+    for (int c = 0; c < KSTEPS; ++c) acc = Ops::mfma(load_vec16<V>(arow + 16 * c), bq[c], acc);
+    return acc;  // acc[v] scores block 32 ch + 8(v/4) + 4 half + v%4
+  };
+
+  // --- Pass 1: a lower bound on L from every fourth chunk. ---------------
+  // The take-th best of any subset of a query's candidates is <= the
+  // take-th best of all of them (L), so every candidate that can matter
+  // scores >= theta = (that value) - 2E - gap. Each lane keeps the K >= take
+  // best of its half of the sample, so the union of the two lists holds the
+  // sample's take best.
+  float theta = -INFINITY;
+  if (n_chunks > 0) {
+    float tk[K];
+#pragma unroll
+    for (int p = 0; p < K; ++p) tk[p] = -INFINITY;
+    for (int ch = 0; ch < n_chunks; ch += 4) {
+      kload(ch);
+      kstore(0);
+      __syncthreads();
+      const floatx16_t acc = score_chunk(0);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        float x = (b < own) ? acc[v] : -INFINITY;
+#pragma unroll
+        for (int p = 0; p < K; ++p) {
+          const float hi = fmaxf(tk[p], x);
+          x = fminf(tk[p], x);
+          tk[p] = hi;
+        }
+      }
+      __syncthreads();
+    }
+    float pk[K];
+#pragma unroll
+    for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
+    float tau = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < 2 * K; ++p) {
+      const float x = p < K ? tk[p] : pk[p - K];
+      int gt = 0, ge = 0;
+#pragma unroll
+      for (int u = 0; u < K; ++u) {
+        gt += (tk[u] > x) + (pk[u] > x);
+        ge += (tk[u] >= x) + (pk[u] >= x);
+      }
+      if (x > -INFINITY && gt < take && take <= ge) tau = x;
+    }
+    if (tau > -INFINITY) theta = tau - 2.f * E - (Ops::kGapRel * (fabsf(tau) + E) + Ops::kGapAbs);
+  }
+
+  // --- Pass 2: every chunk; candidates >= theta that can still enter the
+  // lane's sorted list of the M best are appended to its LDS buffer, and a
+  // buffer about to overflow is folded into the list (the threshold then
+  // rises to the list's M-th best). Chunk ch + 1 waits in registers while
+  // ch is scored; ch + 2 is requested once ch + 1 is in LDS.
   float lv[M];
   int li[M];
 #pragma unroll
   for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
-  int n_in_list = 0;
-
-  if (take > 0 && horizon > 0) {
-    // B operand: this lane's query, features 16c + 8*half + [0, 8).
-    V bq[KSTEPS];
-#pragma unroll
-    for (int c = 0; c < KSTEPS; ++c) {
-      if (live) bq[c] = load_vec16<V>(qrow + 16 * c + 8 * half);
-      else bq[c] = V{};
-    }
-    float thr = -INFINITY;
+  if (n_chunks > 0) {
+    float thr = theta;
     int cnt = 0;
-    const int n_chunks = (horizon + 31) / 32;
-    // A operands of the next chunk are fetched while this one is scored.
-    // Rows past the horizon are clamped to a valid row; their scores are
-    // masked below (every such block is >= own for every query here).
-    V acur[KSTEPS], anext[KSTEPS];
-    {
-      const T* ap = kb + static_cast<int64_t>(min(col, horizon - 1)) * D + 8 * half;
-#pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) acur[c] = load_vec16<V>(ap + 16 * c);
-    }
+    kload(0);
+    kstore(0);
+    if (n_chunks > 1) kload(1);
+    __syncthreads();
     for (int ch = 0; ch < n_chunks; ++ch) {
-      const int blk0 = ch * 32;
-      if (ch + 1 < n_chunks) {
-        const T* ap = kb + static_cast<int64_t>(min(blk0 + 32 + col, horizon - 1)) * D + 8 * half;
-#pragma unroll
-        for (int c = 0; c < KSTEPS; ++c) anext[c] = load_vec16<V>(ap + 16 * c);
-      }
-      floatx16_t acc = {};
-#pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) acc = Ops::mfma(acur[c], bq[c], acc);
-#pragma unroll
-      for (int c = 0; c < KSTEPS; ++c) acur[c] = anext[c];
-      // acc[v] is the score of block blk0 + 8*(v/4) + 4*half + v%4.
+      const floatx16_t acc = score_chunk(ch & 1);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int b = blk0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
         const float a = (b < own) ? acc[v] : -INFINITY;
-        if (a > thr) {
+        if (a >= thr && a > -INFINITY) {
           s_val[wave][cnt][lane] = a;
-          s_idx[wave][cnt][lane] = b;
+          s_idx[wave][cnt][lane] = static_cast<uint16_t>(b);
           ++cnt;
         }
       }
-      // Fold buffers that could overflow on the next chunk.
       if (__any(cnt > CAP - 16)) {
         for (int e = 0; e < cnt; ++e) {
-          const float s = s_val[wave][e][lane];
-          const int j = s_idx[wave][e][lane];
-          if (s > lv[M - 1]) insert_exact<M>(lv, li, s, j);
+          const float sv = s_val[wave][e][lane];
+          if (sv > lv[M - 1]) insert_approx<M>(lv, li, sv, s_idx[wave][e][lane]);
         }
         cnt = 0;
-        thr = lv[M - 1];
+        thr = fmaxf(theta, lv[M - 1]);
       }
+      if (ch + 1 < n_chunks) kstore((ch + 1) & 1);
+      if (ch + 2 < n_chunks) kload(ch + 2);
+      __syncthreads();
     }
     for (int e = 0; e < cnt; ++e) {
-      const float s = s_val[wave][e][lane];
-      const int j = s_idx[wave][e][lane];
-      if (s > lv[M - 1]) insert_exact<M>(lv, li, s, j);
+      const float sv = s_val[wave][e][lane];
+      if (sv > lv[M - 1]) insert_approx<M>(lv, li, sv, s_idx[wave][e][lane]);
     }
-#pragma unroll
-    for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
   }
+  int n_in_list = 0;
+#pragma unroll
+  for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
 
   // --- Merge the two half-lists of this query and decide. -----------------
-  // Rejected candidates of a lane are all <= its M-th best when its list is
-  // full, and there are none otherwise.
+  // Candidates >= theta left out of a lane's list are <= its M-th best (and
+  // there are none while the list is not full); candidates below theta are
+  // checked against the final cut below.
   const float rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
-  const float rej_other = __shfl_xor(rej_mine, 32);
-  const float rej = fmaxf(rej_mine, rej_other);
+  const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
   float pv[M];
+  int pi[M];
 #pragma unroll
-  for (int p = 0; p < M; ++p) pv[p] = __shfl_xor(lv[p], 32);
+  for (int p = 0; p < M; ++p) {
+    pv[p] = __shfl_xor(lv[p], 32);
+    pi[p] = __shfl_xor(li[p], 32);
+  }
   // L = the take-th largest value of the union (a multiset): x is it when
   // fewer than `take` values exceed x and at least `take` reach it.
   float L = -INFINITY;
@@ -445,19 +555,6 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       if (x > -INFINITY && gt < take && take <= ge) L = x;
     }
   }
-  // Error band of this query: E >= |approx - exact| for every candidate.
-  float qn = 0.f;
-  if (live && take > 0) {
-    for (int d = 0; d < D; ++d) {
-      float x = Elem<T>::load(qrow, d);
-      qn += x * x;
-    }
-  }
-  // Accumulation error, plus what flushing denormal operands could drop:
-  // each flushed factor is below kDenorm and its partner below |q| or |kbar|.
-  const float qnorm = sqrtf(qn) * 1.0001f;
-  const float knorm = kbar_norm[r * h_kv + hk];
-  const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
   bool ok = true;
   float cut = -INFINITY;
   if (take > 0 && L > -INFINITY) {
@@ -466,37 +563,43 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     if (!(mag < Ops::kMaxFinite)) ok = false;
     if (rej > -INFINITY && !(L - rej > 2.f * E + gap)) ok = false;
     cut = L - 2.f * E - gap;
+    if (!(cut >= theta)) ok = false;  // a needed candidate may lie below theta
   }
   if (take > 0 && !(E < INFINITY)) ok = false;  // q or kbar carries inf / NaN
-  // Exact rescoring of the surviving candidates of this lane's half.
-  float ev[M];
-  int ei[M];
-#pragma unroll
-  for (int p = 0; p < M; ++p) { ev[p] = -INFINITY; ei[p] = 0x7fffffff; }
-  if (ok && take > 0 && live) {
-#pragma unroll
-    for (int p = 0; p < M; ++p) {
-      if (lv[p] > -INFINITY && lv[p] >= cut) {
-        float s = exact_score(qrow, kb + static_cast<int64_t>(li[p]) * D, D);
-        if (s > -INFINITY) insert_exact<M>(ev, ei, s, li[p]);
-      }
-    }
-  }
-  // Merge with the partner's exact list.
+  // Exact rescoring of every union entry within the band, by the two lanes
+  // together: each forms the exact (float64) partial dot over the features
+  // it holds, and the partials are added. Both lanes walk the union in the
+  // same order (half 0's list first) and keep identical exact lists.
   float fv[M];
   int fi[M];
 #pragma unroll
-  for (int p = 0; p < M; ++p) { fv[p] = ev[p]; fi[p] = ei[p]; }
+  for (int p = 0; p < M; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
+  if (ok && take > 0 && live) {
 #pragma unroll
-  for (int p = 0; p < M; ++p) {
-    const float s = __shfl_xor(ev[p], 32);
-    const int j = __shfl_xor(ei[p], 32);
-    if (s > -INFINITY) insert_exact<M>(fv, fi, s, j);
+    for (int p = 0; p < 2 * M; ++p) {
+      const bool first = (p < M) == (half == 0);
+      const float a = first ? (p < M ? lv[p] : lv[p - M]) : (p < M ? pv[p] : pv[p - M]);
+      const int j = first ? (p < M ? li[p] : li[p - M]) : (p < M ? pi[p] : pi[p - M]);
+      if (a > -INFINITY && a >= cut) {
+        const T* krow = kb + static_cast<int64_t>(j) * D + 8 * half;
+        double part = 0.0;
+#pragma unroll
+        for (int c = 0; c < KSTEPS; ++c) {
+          const V kv = load_vec16<V>(krow + 16 * c);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            part += static_cast<double>(static_cast<float>(bq[c][i])) *
+                    static_cast<double>(static_cast<float>(kv[i]));
+        }
+        part += __shfl_xor(part, 32);
+        const float sc = Elem<T>::round(static_cast<float>(part));
+        if (sc > -INFINITY) insert_exact<M>(fv, fi, sc, j);
+      }
+    }
   }
-  const int ok_all = (ok ? 1 : 0) & __shfl_xor(ok ? 1 : 0, 32);
   if (!live || half != 0) return;
   const int64_t qid = hm_query(packed, r, hq, h_q, S, tok, t);
-  if (!ok_all) {
+  if (!ok) {
     const int slot = atomicAdd(queue_len, 1);
     queue[slot] = (r * h_q + hq) * rows_per_seq + t;
     return;
@@ -554,9 +657,11 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
                        hipStream_t st) {
   constexpr int WAVES = 4;
   constexpr int CAP = M + 24;
+  constexpr int K = M <= 12 ? 8 : 16;  // sample list per lane: K >= take, so the
+                                      // union holds the sample's take best
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq, 32 * WAVES)),
             static_cast<unsigned>(g.rows * g.h_q));
-  hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, CAP, WAVES>), grid, dim3(64 * WAVES), 0, st,
+  hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, K, CAP, WAVES>), grid, dim3(64 * WAVES), 0, st,
                      static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
                      g.seq_len, g.h_q, g.h_kv, g.n_blocks, static_cast<int>(g.block_size),
                      take, cur, static_cast<int>(g.slots), ws.kbar_norm, ws.queue,
@@ -572,7 +677,9 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
     (void)workspace; (void)ws_bytes;
     return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, nullptr, nullptr, st);
   } else {
-  const bool mfma_ok = (g.head_dim == 64 || g.head_dim == 128) && take <= 16;
+  // Block ids travel through LDS as 16 bits in the MFMA kernel.
+  const bool mfma_ok = (g.head_dim == 64 || g.head_dim == 128) && take <= 16 &&
+                       g.n_blocks <= 65535;
   if (!mfma_ok) return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, nullptr, nullptr, st);
   const int64_t qcap = g.rows * g.h_q * g.rows_per_seq;
   if (!workspace || ws_bytes < moba_gate_workspace_size(g.rows, g.rows_per_seq, g.h_q) ||

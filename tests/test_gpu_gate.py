@@ -115,3 +115,15 @@ def test_gate_full_size_config2(device):
     cfg = MoBAConfig(block_size=128, top_k=8)
     q, k, _ = make_qkv((1, 65536, 4, 64), torch.bfloat16, seed=0, device=device)
     check(q, k, cfg)
+
+
+@pytest.mark.parametrize("d,bs,tk", [(64, 128, 8), (128, 64, 8), (64, 32, 13)])
+def test_gate_integer_inputs_with_many_exact_ties(device, d, bs, tk):
+    """Small-integer q and k make equal scores common: the lowest-index
+    tie-break and the approximate-then-exact retention must still agree with
+    the oracle bit for bit (many queries take the exact fallback here)."""
+    cfg = MoBAConfig(block_size=bs, top_k=tk)
+    g = torch.Generator().manual_seed(21)
+    q = torch.randint(-2, 3, (1, 8192, 2, d), generator=g).to(torch.bfloat16).to(device)
+    k = torch.randint(-1, 2, (1, 8192, 2, d), generator=g).to(torch.bfloat16).to(device)
+    check(q, k, cfg)
