@@ -242,7 +242,7 @@ int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hip
 // Backward (bwd_mfma_kernel): one workgroup per (KV block, row * kv head),
 // one wave per 32 keys of the block. The workgroup owns its keys' dK / dV
 // for the whole column (registers, stored once: no atomics), and walks the
-// column in groups of 32 entries. Per group, with the group's Q / dO staged
+// column in steps of 64 entries. Per step, with the step's Q / dO staged
 // in LDS in both orientations:
 //
 //   S[q][key]   = Q . K^T,   dP[q][key] = dO . V^T      (lane <-> key)
@@ -255,29 +255,31 @@ int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hip
 // inside the workgroup, so the partial buffer is [.., slots, D], not
 // slots x sub-tiles. Semantics: src/moba/kernels/moba_bwd.py:216-394.
 // ---------------------------------------------------------------------------
-template <typename T, typename A, int D, int BS>
+template <typename T, typename A, int D, int BS, int NQ>
 __global__ void __launch_bounds__(BS * 2, 1)
 bwd_mfma_kernel(AttnArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec;
   using Sc = typename M::scalar;
+  // NQ: queries per step (64 at head_dim 64; 32 at 128 to fit LDS)
+  constexpr int QT = NQ / 32;   // query tiles of 32
   constexpr int NW = BS / 32;   // waves: 32 keys each
   constexpr int NT = NW * 64;   // threads
   constexpr int DT = D / 32;
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
   constexpr int KTS = BS + 8;   // row stride of K^T and dS ([*][key])
-  constexpr int QTS = 32 + 8;   // row stride of Q^T / dO^T ([d][q])
+  constexpr int QTS = NQ + 8;   // row stride of Q^T / dO^T ([d][q])
   __shared__ __attribute__((aligned(16))) uint16_t Ks[BS * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[BS * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[32 * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Os[32 * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[NQ * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Os[NQ * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Qt[D * QTS];
   __shared__ __attribute__((aligned(16))) uint16_t Ot[D * QTS];
-  __shared__ __attribute__((aligned(16))) uint16_t DS[32 * KTS];
-  __shared__ float s_lse[32], s_delta[32];
-  __shared__ int s_lim[32];
-  __shared__ int64_t s_dst[32];
+  __shared__ __attribute__((aligned(16))) uint16_t DS[NQ * KTS];
+  __shared__ float s_lse[NQ], s_delta[NQ];
+  __shared__ int s_lim[NQ];
+  __shared__ int64_t s_dst[NQ];
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
   const int tid = threadIdx.x;
@@ -313,28 +315,31 @@ bwd_mfma_kernel(AttnArgs a) {
   for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
   A* dq_out = static_cast<A*>(a.part_acc);
 
-  // The next group's entry metadata and Q / dO rows are fetched into
-  // registers while the current group is computed, then written to LDS.
-  constexpr int CH = (32 * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per tensor
+  // The next step's entry metadata and Q / dO rows are fetched into
+  // registers while the current step is computed, then written to LDS.
+  constexpr int CH = (NQ * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per tensor
+  constexpr int MT = (NQ + NT - 1) / NT;          // metadata entries per thread
   uint4 pq[CH], po[CH];
-  int p_lim = -1;
-  float p_lse = 0.f, p_dl = 0.f;
-  int64_t p_dst = -1;
+  int p_lim[MT];
+  float p_lse[MT], p_dl[MT];
+  int64_t p_dst[MT];
   auto fetch = [&](int32_t g0) {
-    if (tid < 32) {
-      const int32_t e = g0 + tid;
-      p_lim = -1; p_lse = 0.f; p_dl = 0.f; p_dst = -1;
-      if (e < c.n) {
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int qi = tid + u * NT;
+      const int32_t e = g0 + qi;
+      p_lim[u] = -1; p_lse[u] = 0.f; p_dl[u] = 0.f; p_dst[u] = -1;
+      if (qi < NQ && e < c.n) {
         const int32_t row = a.row_indices[c.lo + e];
         const int32_t head = a.head_indices[c.lo + e];
         const int32_t slot = a.slot_of_pair[c.lo + e];
         const int64_t pr = part_row(a, c, row, head);
-        p_lse = a.lse[pr];
-        p_dl = a.delta[pr];
-        p_dst = pr * a.slots + slot;
+        p_lse[u] = a.lse[pr];
+        p_dl[u] = a.delta[pr];
+        p_dst[u] = pr * a.slots + slot;
         const int64_t rrel = static_cast<int64_t>(row) - c.key0;
         const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
-        p_lim = min(key_lim - 1, row_lim);
+        p_lim[u] = min(key_lim - 1, row_lim);
       }
     }
 #pragma unroll
@@ -342,7 +347,7 @@ bwd_mfma_kernel(AttnArgs a) {
       const int i = tid + u * NT;
       pq[u] = make_uint4(0, 0, 0, 0);
       po[u] = make_uint4(0, 0, 0, 0);
-      if (i < 32 * D / 8) {
+      if (i < NQ * D / 8) {
         const int32_t e = g0 + i / (D / 8);
         if (e < c.n) {
           const int32_t row = a.row_indices[c.lo + e];
@@ -356,20 +361,24 @@ bwd_mfma_kernel(AttnArgs a) {
   };
   fetch(0);
 
-  for (int32_t g0 = 0; g0 < c.n; g0 += 32) {
-    __syncthreads();  // previous group fully consumed (and K / V staged)
-    if (tid < 32) {
-      s_lim[tid] = p_lim;
-      s_lse[tid] = p_lse;
-      s_delta[tid] = p_dl;
-      s_dst[tid] = p_dst;
+  for (int32_t g0 = 0; g0 < c.n; g0 += NQ) {
+    __syncthreads();  // previous step fully consumed (and K / V staged)
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int qi = tid + u * NT;
+      if (qi < NQ) {
+        s_lim[qi] = p_lim[u];
+        s_lse[qi] = p_lse[u];
+        s_delta[qi] = p_dl[u];
+        s_dst[qi] = p_dst[u];
+      }
     }
-    // Q and dO rows of the group: row-major and transposed (q permuted per
-    // 16-slice so each lane-half's eight queries are contiguous).
+    // Q and dO rows: row-major and transposed (q permuted per 16-slice so
+    // each lane-half's eight queries of a K-step are contiguous).
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = tid + u * NT;
-      if (i < 32 * D / 8) {
+      if (i < NQ * D / 8) {
         const int q = i / (D / 8);
         const int d8 = (i % (D / 8)) * 8;
         *reinterpret_cast<uint4*>(&Qs[q * RS + d8]) = pq[u];
@@ -385,51 +394,55 @@ bwd_mfma_kernel(AttnArgs a) {
       }
     }
     __syncthreads();
-    if (g0 + 32 < c.n) fetch(g0 + 32);
+    if (g0 + NQ < c.n) fetch(g0 + NQ);
 
-    // S and dP for this wave's 32 keys; lane <-> key, register v <-> query
-    // 8(v/4) + 4h + v%4.
-    floatx16_t sacc = floatx16_t{}, pacc = floatx16_t{};
-    {
-      const uint16_t* qa = &Qs[col * RS + 8 * h];
-      const uint16_t* oa = &Os[col * RS + 8 * h];
-      const uint16_t* kb = &Ks[mykey * RS + 8 * h];
-      const uint16_t* vb = &Vs[mykey * RS + 8 * h];
+    // S and dP for this wave's 32 keys and each 32-query tile; lane <->
+    // key, register v <-> query 32 qt + 8(v/4) + 4h + v%4.
+    const uint16_t* kb = &Ks[mykey * RS + 8 * h];
+    const uint16_t* vb = &Vs[mykey * RS + 8 * h];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      floatx16_t sacc = floatx16_t{}, pacc = floatx16_t{};
+      const uint16_t* qa = &Qs[(qt * 32 + col) * RS + 8 * h];
+      const uint16_t* oa = &Os[(qt * 32 + col) * RS + 8 * h];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
         sacc = M::mma(ld16<V8>(qa + 16 * k), ld16<V8>(kb + 16 * k), sacc);
         pacc = M::mma(ld16<V8>(oa + 16 * k), ld16<V8>(vb + 16 * k), pacc);
       }
-    }
-    V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
+      V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int q = 8 * (v >> 2) + 4 * h + (v & 3);
-      const bool ok = mykey <= s_lim[q];
-      const float p = ok ? __builtin_amdgcn_exp2f(sacc[v] * a.scale_log2 - s_lse[q]) : 0.f;
-      const float ds = p * (pacc[v] - s_delta[q]);
-      pb[v >> 3][v & 7] = static_cast<Sc>(p);
-      db[v >> 3][v & 7] = static_cast<Sc>(ds);
-      DS[q * KTS + mykey] = __builtin_bit_cast(uint16_t, static_cast<Sc>(ds));
-    }
+      for (int v = 0; v < 16; ++v) {
+        const int q = qt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        const bool ok = mykey <= s_lim[q];
+        const float p = ok ? __builtin_amdgcn_exp2f(sacc[v] * a.scale_log2 - s_lse[q]) : 0.f;
+        const float ds = p * (pacc[v] - s_delta[q]);
+        pb[v >> 3][v & 7] = static_cast<Sc>(p);
+        db[v >> 3][v & 7] = static_cast<Sc>(ds);
+        DS[q * KTS + mykey] = __builtin_bit_cast(uint16_t, static_cast<Sc>(ds));
+      }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 2; ++j) {
+        const int qoff = qt * 32 + 16 * j + 8 * h;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        dv[dt] = M::mma(ld16<V8>(&Ot[(dt * 32 + col) * QTS + 16 * j + 8 * h]), pb[j], dv[dt]);
-        dk[dt] = M::mma(ld16<V8>(&Qt[(dt * 32 + col) * QTS + 16 * j + 8 * h]), db[j], dk[dt]);
+        for (int dt = 0; dt < DT; ++dt) {
+          dv[dt] = M::mma(ld16<V8>(&Ot[(dt * 32 + col) * QTS + qoff]), pb[j], dv[dt]);
+          dk[dt] = M::mma(ld16<V8>(&Qt[(dt * 32 + col) * QTS + qoff]), db[j], dk[dt]);
+        }
       }
     }
     __syncthreads();  // dS of every wave visible
 
-    // dQ^T[d][q] over all BS keys; tiles of 32 features spread over waves.
-    for (int dt = wave; dt < DT; dt += NW) {
+    // dQ^T[d][q] over all BS keys; (feature tile, query tile) pairs spread
+    // over the waves.
+    for (int tt = wave; tt < DT * QT; tt += NW) {
+      const int dt = tt % DT, qt = tt / DT;
       floatx16_t dq = floatx16_t{};
 #pragma unroll
       for (int j = 0; j < BS / 16; ++j)
         dq = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
-                    ld16<V8>(&DS[col * KTS + 16 * j + 8 * h]), dq);
-      const int64_t dst = s_dst[col];
+                    ld16<V8>(&DS[(qt * 32 + col) * KTS + 16 * j + 8 * h]), dq);
+      const int64_t dst = s_dst[qt * 32 + col];
       if (dst >= 0) {
         A* base = dq_out + dst * D + dt * 32 + 4 * h;
 #pragma unroll
@@ -459,8 +472,9 @@ bwd_mfma_kernel(AttnArgs a) {
 
 template <typename T, typename A, int D, int BS>
 static int launch_bwd(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
+  constexpr int NQ = D == 128 ? 32 : 64;
   dim3 grid(static_cast<unsigned>(a.n_blocks), static_cast<unsigned>(n_cols));
-  hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS>), grid, dim3(BS * 2), 0, st, a);
+  hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS, NQ>), grid, dim3(BS * 2), 0, st, a);
   return check_launch("moba_bwd (mfma)");
 }
 

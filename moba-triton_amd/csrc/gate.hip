@@ -98,9 +98,24 @@ gate_prep_kernel(const T* __restrict__ kbar, const int32_t* __restrict__ cu,
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ inline float exact_score(const T* __restrict__ q, const T* __restrict__ kb, int D) {
+  // Products of two bf16/fp16/fp32 values are exact in float64, and so is
+  // the sum for any realistic input; it is rounded once to float32 and once
+  // to the storage dtype, like the oracle's scores.
   double acc = 0.0;
-  for (int d = 0; d < D; ++d)
-    acc += static_cast<double>(Elem<T>::load(q, d)) * static_cast<double>(Elem<T>::load(kb, d));
+  if constexpr (sizeof(T) == 2) {
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      const uint4 qa = *reinterpret_cast<const uint4*>(q + d0);
+      const uint4 ka = *reinterpret_cast<const uint4*>(kb + d0);
+      const T* qe = reinterpret_cast<const T*>(&qa);
+      const T* ke = reinterpret_cast<const T*>(&ka);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        acc += static_cast<double>(Elem<T>::load(qe, i)) * static_cast<double>(Elem<T>::load(ke, i));
+    }
+  } else {
+    for (int d = 0; d < D; ++d)
+      acc += static_cast<double>(Elem<T>::load(q, d)) * static_cast<double>(Elem<T>::load(kb, d));
+  }
   return Elem<T>::round(static_cast<float>(acc));
 }
 
@@ -140,6 +155,26 @@ __device__ inline void insert_approx(float (&val)[M], int (&idx)[M], float s, in
     val[p] = nv;
     idx[p] = ni;
   }
+}
+
+// k-th largest (1-based, k <= M) of the union of two lists sorted in
+// descending order: max over i of min(A[i-1], B[k-i-1]), an entry past either
+// end counting as +inf. -inf when the union holds fewer than k finite values.
+template <int M>
+__device__ inline float kth_of_union(const float (&A)[M], const float (&B)[M], int k) {
+  float best = -INFINITY;
+#pragma unroll
+  for (int i = 0; i <= M; ++i) {
+    if (i > k) break;
+    const float a = i == 0 ? INFINITY : A[i - 1];
+    const int jb = k - i;
+    float b = INFINITY;
+#pragma unroll
+    for (int u = 0; u < M; ++u) b = (u == jb - 1) ? B[u] : b;
+    if (jb > M) b = -INFINITY;
+    best = fmaxf(best, fminf(a, b));
+  }
+  return best;
 }
 
 // Emits own block + selected ids ascending, -1 padded, into `out[0..slots)`.
@@ -248,12 +283,16 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                   int64_t S, int64_t rows_per_seq, int64_t h_q, int64_t h_kv,
                   int D, int64_t n_blocks, int bs, int take, int cur, int slots,
                   const int64_t* __restrict__ queue, const int* __restrict__ queue_len) {
+  // One workgroup per queued query: 256 lanes split its candidates, each
+  // keeps an exact top-T list, the lists merge with a butterfly inside each
+  // wave and then across the four waves through LDS.
+  __shared__ float s_v[4][TMAX];
+  __shared__ int s_i[4][TMAX];
   const int lane = threadIdx.x & 63;
-  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (blockDim.x / 64);
+  const int wave = threadIdx.x >> 6;
   const int64_t total = *queue_len;
   const bool packed = cu != nullptr;
-  for (int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
-       item < total; item += n_waves) {
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
     const int64_t code = queue[item];  // (r * h_q + hq) * rows_per_seq + t
     const int64_t t = code % rows_per_seq;
     const int64_t rh = code / rows_per_seq;
@@ -267,7 +306,7 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     int idx[TMAX];
 #pragma unroll
     for (int p = 0; p < TMAX; ++p) { val[p] = -INFINITY; idx[p] = 0x7fffffff; }
-    for (int j = lane; j < own; j += 64) {
+    for (int j = threadIdx.x; j < own; j += blockDim.x) {
       const float s = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
       if (ranks_before(s, j, val[take - 1], idx[take - 1])) insert_exact<TMAX>(val, idx, s, j);
     }
@@ -284,6 +323,15 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
         if (pv[p] > -INFINITY) insert_exact<TMAX>(val, idx, pv[p], pi[p]);
     }
     if (lane == 0) {
+#pragma unroll
+      for (int p = 0; p < TMAX; ++p) { s_v[wave][p] = val[p]; s_i[wave][p] = idx[p]; }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < 4; ++w)
+#pragma unroll
+        for (int p = 0; p < TMAX; ++p)
+          if (s_v[w][p] > -INFINITY) insert_exact<TMAX>(val, idx, s_v[w][p], s_i[w][p]);
       int n_sel = 0;
 #pragma unroll
       for (int p = 0; p < TMAX; ++p)
@@ -291,6 +339,7 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
                         out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
     }
+    __syncthreads();
   }
 }
 
@@ -433,9 +482,12 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // --- Pass 1: a lower bound on L from every fourth chunk. ---------------
   // The take-th best of any subset of a query's candidates is <= the
   // take-th best of all of them (L), so every candidate that can matter
-  // scores >= theta = (that value) - 2E - gap. Each lane keeps the K >= take
-  // best of its half of the sample, so the union of the two lists holds the
-  // sample's take best.
+  // scores >= theta = (that value) - 2E - gap. Each lane keeps the K best of
+  // its half of the sample; the take-th best of the union of the two lists
+  // is the take-th best of a subset of the sample, so it bounds L as well.
+  // Lane 0 of the wave holds its smallest query, so its own block bounds
+  // every lane's: chunks entirely below it need no causal mask.
+  const int own_min = __builtin_amdgcn_readfirstlane(own);
   float theta = -INFINITY;
   if (n_chunks > 0) {
     float tk[K];
@@ -446,10 +498,11 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       kstore(0);
       __syncthreads();
       const floatx16_t acc = score_chunk(0);
+      const bool full = ch * 32 + 32 <= own_min;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        float x = (b < own) ? acc[v] : -INFINITY;
+        float x = (full || b < own) ? acc[v] : -INFINITY;
 #pragma unroll
         for (int p = 0; p < K; ++p) {
           const float hi = fmaxf(tk[p], x);
@@ -462,20 +515,11 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     float pk[K];
 #pragma unroll
     for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
-    float tau = -INFINITY;
-#pragma unroll
-    for (int p = 0; p < 2 * K; ++p) {
-      const float x = p < K ? tk[p] : pk[p - K];
-      int gt = 0, ge = 0;
-#pragma unroll
-      for (int u = 0; u < K; ++u) {
-        gt += (tk[u] > x) + (pk[u] > x);
-        ge += (tk[u] >= x) + (pk[u] >= x);
-      }
-      if (x > -INFINITY && gt < take && take <= ge) tau = x;
-    }
+    const float tau = kth_of_union<K>(tk, pk, take);
     if (tau > -INFINITY) theta = tau - 2.f * E - (Ops::kGapRel * (fabsf(tau) + E) + Ops::kGapAbs);
   }
+  // Collection threshold: a > thr0 is a >= theta.
+  const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
   // --- Pass 2: every chunk; candidates >= theta that can still enter the
   // lane's sorted list of the M best are appended to its LDS buffer, and a
@@ -487,7 +531,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
   for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
   if (n_chunks > 0) {
-    float thr = theta;
+    float thr = thr0;
     int cnt = 0;
     kload(0);
     kstore(0);
@@ -495,14 +539,26 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     __syncthreads();
     for (int ch = 0; ch < n_chunks; ++ch) {
       const floatx16_t acc = score_chunk(ch & 1);
+      if (ch * 32 + 32 <= own_min) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        const float a = (b < own) ? acc[v] : -INFINITY;
-        if (a >= thr && a > -INFINITY) {
-          s_val[wave][cnt][lane] = a;
-          s_idx[wave][cnt][lane] = static_cast<uint16_t>(b);
-          ++cnt;
+        for (int v = 0; v < 16; ++v) {
+          if (acc[v] > thr) {
+            s_val[wave][cnt][lane] = acc[v];
+            s_idx[wave][cnt][lane] =
+                static_cast<uint16_t>(ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3));
+            ++cnt;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+          const float a = (b < own) ? acc[v] : -INFINITY;
+          if (a > thr) {
+            s_val[wave][cnt][lane] = a;
+            s_idx[wave][cnt][lane] = static_cast<uint16_t>(b);
+            ++cnt;
+          }
         }
       }
       if (__any(cnt > CAP - 16)) {
@@ -511,7 +567,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
           if (sv > lv[M - 1]) insert_approx<M>(lv, li, sv, s_idx[wave][e][lane]);
         }
         cnt = 0;
-        thr = fmaxf(theta, lv[M - 1]);
+        thr = fmaxf(thr0, lv[M - 1]);
       }
       if (ch + 1 < n_chunks) kstore((ch + 1) & 1);
       if (ch + 2 < n_chunks) kload(ch + 2);
@@ -539,22 +595,8 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     pv[p] = __shfl_xor(lv[p], 32);
     pi[p] = __shfl_xor(li[p], 32);
   }
-  // L = the take-th largest value of the union (a multiset): x is it when
-  // fewer than `take` values exceed x and at least `take` reach it.
-  float L = -INFINITY;
-  if (take > 0) {
-#pragma unroll
-    for (int p = 0; p < 2 * M; ++p) {
-      const float x = p < M ? lv[p] : pv[p - M];
-      int gt = 0, ge = 0;
-#pragma unroll
-      for (int u = 0; u < M; ++u) {
-        gt += (lv[u] > x) + (pv[u] > x);
-        ge += (lv[u] >= x) + (pv[u] >= x);
-      }
-      if (x > -INFINITY && gt < take && take <= ge) L = x;
-    }
-  }
+  // L = the take-th largest approximate score of the union.
+  const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
   bool ok = true;
   float cut = -INFINITY;
   if (take > 0 && L > -INFINITY) {
@@ -657,8 +699,9 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
                        hipStream_t st) {
   constexpr int WAVES = 4;
   constexpr int CAP = M + 24;
-  constexpr int K = M <= 12 ? 8 : 16;  // sample list per lane: K >= take, so the
-                                      // union holds the sample's take best
+  // Sample list per lane: the take-th best of the union of both lanes'
+  // lists (2K >= take) is the take-th best of some subset of the sample.
+  constexpr int K = M <= 12 ? 5 : 9;
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq, 32 * WAVES)),
             static_cast<unsigned>(g.rows * g.h_q));
   hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, K, CAP, WAVES>), grid, dim3(64 * WAVES), 0, st,
@@ -703,13 +746,13 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   // Queries whose approximate evidence was insufficient: exact rescoring,
   // one wave per query.
   if (take <= 8)
-    hipLaunchKernelGGL((gate_queue_kernel<T, 8>), dim3(1024), dim3(256), 0, st,
+    hipLaunchKernelGGL((gate_queue_kernel<T, 8>), dim3(2048), dim3(256), 0, st,
                        static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
                        g.seq_len, g.rows_per_seq, g.h_q, g.h_kv, static_cast<int>(g.head_dim),
                        g.n_blocks, static_cast<int>(g.block_size), take, cur,
                        static_cast<int>(g.slots), ws.queue, ws.counter);
   else
-    hipLaunchKernelGGL((gate_queue_kernel<T, 16>), dim3(1024), dim3(256), 0, st,
+    hipLaunchKernelGGL((gate_queue_kernel<T, 16>), dim3(2048), dim3(256), 0, st,
                        static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
                        g.seq_len, g.rows_per_seq, g.h_q, g.h_kv, static_cast<int>(g.head_dim),
                        g.n_blocks, static_cast<int>(g.block_size), take, cur,
@@ -740,6 +783,8 @@ extern "C" int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
   if (!q || !kbar || !block_idx) return fail(MOBA_ERR_INVALID, "null pointer");
   if (take < 0 || slots < take + (always_current ? 1 : 0))
     return fail(MOBA_ERR_INVALID, "slots must hold take (+1 with the own block)");
+  if (head_dim % 8 != 0)
+    return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
   if (g.rows_per_seq >= (int64_t(1) << 31) / 2)
     return fail(MOBA_ERR_UNSUPPORTED, "sequence too long for int32 block ids");
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
