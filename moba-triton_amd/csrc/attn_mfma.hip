@@ -118,19 +118,31 @@ attend_mfma_kernel(AttnArgs a) {
   const int col = lane & 31;
   A* acc_out = static_cast<A*>(a.part_acc);
 
-  for (int32_t g0 = wave * 32; g0 < c.n; g0 += 4 * 32) {
+  // The next group's entry and Q row are fetched while this one is computed.
+  int32_t n_row = 0, n_head = 0, n_slot = 0;
+  bool n_live = false;
+  V8 nq[D / 16];
+  auto fetch = [&](int32_t g0) {
     const int32_t e = g0 + col;
-    const bool live = e < c.n;
-    const int32_t row = live ? a.row_indices[c.lo + e] : 0;
-    const int32_t head = live ? a.head_indices[c.lo + e] : 0;
-    const int32_t slot = live ? a.slot_of_pair[c.lo + e] : 0;
-
-    // B operand: this lane's query, features 16k + 8h + [0, 8).
-    V8 bq[D / 16];
-    const uint16_t* qrow = Q + q_offset(a, c, row, head);
+    n_live = e < c.n;
+    n_row = n_live ? a.row_indices[c.lo + e] : 0;
+    n_head = n_live ? a.head_indices[c.lo + e] : 0;
+    n_slot = n_live ? a.slot_of_pair[c.lo + e] : 0;
+    const uint16_t* qrow = Q + q_offset(a, c, n_row, n_head);
 #pragma unroll
     for (int k = 0; k < D / 16; ++k)
-      bq[k] = live ? ld16<V8>(qrow + 16 * k + 8 * h) : V8{};
+      nq[k] = n_live ? ld16<V8>(qrow + 16 * k + 8 * h) : V8{};
+  };
+  if (wave * 32 < c.n) fetch(wave * 32);
+
+  for (int32_t g0 = wave * 32; g0 < c.n; g0 += 4 * 32) {
+    const bool live = n_live;
+    const int32_t row = n_row, head = n_head, slot = n_slot;
+    // B operand: this lane's query, features 16k + 8h + [0, 8).
+    V8 bq[D / 16];
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) bq[k] = nq[k];
+    if (g0 + 4 * 32 < c.n) fetch(g0 + 4 * 32);
 
     floatx16_t s[KT];
 #pragma unroll
@@ -256,7 +268,7 @@ int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hip
 // slots x sub-tiles. Semantics: src/moba/kernels/moba_bwd.py:216-394.
 // ---------------------------------------------------------------------------
 template <typename T, typename A, int D, int BS, int NQ>
-__global__ void __launch_bounds__(BS * 2, 1)
+__global__ void __launch_bounds__(BS * 2, (D == 64 && BS == 128) ? 2 : 1)
 bwd_mfma_kernel(AttnArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec;
@@ -269,8 +281,6 @@ bwd_mfma_kernel(AttnArgs a) {
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
   constexpr int KTS = BS + 8;   // row stride of K^T and dS ([*][key])
   constexpr int QTS = NQ + 8;   // row stride of Q^T / dO^T ([d][q])
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BS * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[BS * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
   __shared__ __attribute__((aligned(16))) uint16_t Qs[NQ * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Os[NQ * RS];
@@ -289,17 +299,14 @@ bwd_mfma_kernel(AttnArgs a) {
   const uint16_t* Og = static_cast<const uint16_t*>(a.dout);
   const int key_lim = static_cast<int>(c.key_end - c.key0);
 
+  // K^T of the block in LDS (for dQ); K and V rows of this lane's key stay
+  // in registers as the B operands of S and dP for the whole column.
   for (int i = tid; i < BS * D / 8; i += NT) {
     const int key = i / (D / 8);
     const int d8 = (i % (D / 8)) * 8;
-    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-    if (key < key_lim) {
-      const int64_t off = ((c.tok0 + key) * a.h_kv + c.hk) * D + d8;
-      kv = *reinterpret_cast<const uint4*>(Kg + off);
-      vv = *reinterpret_cast<const uint4*>(Vg + off);
-    }
-    *reinterpret_cast<uint4*>(&Ks[key * RS + d8]) = kv;
-    *reinterpret_cast<uint4*>(&Vs[key * RS + d8]) = vv;
+    uint4 kv = make_uint4(0, 0, 0, 0);
+    if (key < key_lim)
+      kv = *reinterpret_cast<const uint4*>(Kg + ((c.tok0 + key) * a.h_kv + c.hk) * D + d8);
     const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kv);
 #pragma unroll
     for (int u = 0; u < 8; ++u) Kt[(d8 + u) * KTS + key] = ke[u];
@@ -310,6 +317,16 @@ bwd_mfma_kernel(AttnArgs a) {
   const int h = lane >> 5;
   const int col = lane & 31;
   const int mykey = wave * 32 + col;  // the key this lane holds in S / dP / dV / dK
+  V8 kb[D / 16], vb[D / 16];
+  {
+    const bool kok = mykey < key_lim;
+    const int64_t off = ((c.tok0 + mykey) * a.h_kv + c.hk) * D + 8 * h;
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) {
+      kb[k] = kok ? ld16<V8>(Kg + off + 16 * k) : V8{};
+      vb[k] = kok ? ld16<V8>(Vg + off + 16 * k) : V8{};
+    }
+  }
   floatx16_t dv[DT], dk[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
@@ -398,8 +415,6 @@ bwd_mfma_kernel(AttnArgs a) {
 
     // S and dP for this wave's 32 keys and each 32-query tile; lane <->
     // key, register v <-> query 32 qt + 8(v/4) + 4h + v%4.
-    const uint16_t* kb = &Ks[mykey * RS + 8 * h];
-    const uint16_t* vb = &Vs[mykey * RS + 8 * h];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       floatx16_t sacc = floatx16_t{}, pacc = floatx16_t{};
@@ -407,8 +422,8 @@ bwd_mfma_kernel(AttnArgs a) {
       const uint16_t* oa = &Os[(qt * 32 + col) * RS + 8 * h];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
-        sacc = M::mma(ld16<V8>(qa + 16 * k), ld16<V8>(kb + 16 * k), sacc);
-        pacc = M::mma(ld16<V8>(oa + 16 * k), ld16<V8>(vb + 16 * k), pacc);
+        sacc = M::mma(ld16<V8>(qa + 16 * k), kb[k], sacc);
+        pacc = M::mma(ld16<V8>(oa + 16 * k), vb[k], pacc);
       }
       V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
 #pragma unroll
