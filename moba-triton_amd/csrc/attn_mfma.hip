@@ -27,6 +27,7 @@ namespace moba {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte chunk
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16_t> {
@@ -84,8 +85,13 @@ attend_mfma_kernel(AttnArgs a) {
   constexpr int VS = BS + 8;   // V^T row stride
   constexpr int KT = BS / 32;  // key tiles of 32
   constexpr int DT = D / 32;   // head_dim tiles of 32
+  constexpr int RQ = D / 8;    // 16-byte chunks per row
+  constexpr int CH = 32 * RQ / 64;  // 16-byte chunks per lane per 32-row tile
+  constexpr bool kWide = sizeof(A) == 2;  // 16-bit partials go out through LDS as rows
   __shared__ __attribute__((aligned(16))) uint16_t Ks[BS * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
+  // Per wave: the group's Q rows on the way in, its partial rows on the way out.
+  __shared__ __attribute__((aligned(16))) uint16_t Rw[4][32 * KS];
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
   if (c.n == 0) return;
@@ -116,33 +122,63 @@ attend_mfma_kernel(AttnArgs a) {
   const int wave = tid >> 6;
   const int h = lane >> 5;
   const int col = lane & 31;
+  uint16_t* rw = Rw[wave];
   A* acc_out = static_cast<A*>(a.part_acc);
 
-  // The next group's entry and Q row are fetched while this one is computed.
-  int32_t n_row = 0, n_head = 0, n_slot = 0;
-  bool n_live = false;
-  V8 nq[D / 16];
-  auto fetch = [&](int32_t g0) {
-    const int32_t e = g0 + col;
-    n_live = e < c.n;
-    n_row = n_live ? a.row_indices[c.lo + e] : 0;
-    n_head = n_live ? a.head_indices[c.lo + e] : 0;
-    n_slot = n_live ? a.slot_of_pair[c.lo + e] : 0;
-    const uint16_t* qrow = Q + q_offset(a, c, n_row, n_head);
-#pragma unroll
-    for (int k = 0; k < D / 16; ++k)
-      nq[k] = n_live ? ld16<V8>(qrow + 16 * k + 8 * h) : V8{};
+  // Rows move in whole 16-byte chunks: lane i of the wave carries chunk
+  // i % RQ of rows i / RQ + (64 / RQ) u, so every load / store instruction
+  // covers complete rows. Two-stage pipeline: while group g is computed the
+  // Q rows of group g + 1 and the index entries of group g + 2 are in flight.
+  // Lane col holds the entries of query g + col; slot < 0 marks a dead lane.
+  auto load_idx = [&](int32_t g, int32_t& r, int32_t& hd, int32_t& sl) {
+    // Unconditional loads (clamped entry) keep the wait counts static.
+    const int32_t e = g + col;
+    const int64_t i = c.lo + (e < c.n ? e : c.n - 1);
+    r = a.row_indices[i];
+    hd = a.head_indices[i];
+    sl = e < c.n ? a.slot_of_pair[i] : -1;
   };
-  if (wave * 32 < c.n) fetch(wave * 32);
+  u32x4 nq[CH];
+  auto q_off = [&](int32_t r, int32_t hd, int32_t sl) -> int64_t {
+    return sl >= 0 ? q_offset(a, c, r, hd) : -1;
+  };
+  auto fetch = [&](int64_t off) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int64_t o = __shfl(off, lane / RQ + (64 / RQ) * u);
+      nq[u] = u32x4{0, 0, 0, 0};
+      if (o >= 0) nq[u] = *reinterpret_cast<const u32x4*>(Q + o + (lane % RQ) * 8);
+    }
+  };
+  int32_t cr, chd, csl, nr, nhd, nsl;
+  load_idx(wave * 32, cr, chd, csl);
+  fetch(q_off(cr, chd, csl));
+  load_idx(wave * 32 + 128, nr, nhd, nsl);
+  auto stage_q = [&]() {
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      *reinterpret_cast<u32x4*>(&rw[(lane / RQ + (64 / RQ) * u) * KS + (lane % RQ) * 8]) = nq[u];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  stage_q();
+  int64_t noff = q_off(nr, nhd, nsl);
 
   for (int32_t g0 = wave * 32; g0 < c.n; g0 += 4 * 32) {
-    const bool live = n_live;
-    const int32_t row = n_row, head = n_head, slot = n_slot;
+    const bool live = csl >= 0;
+    const int32_t row = cr;
+    const int32_t head = chd;
+    const int32_t slot = csl;
     // B operand: this lane's query, features 16k + 8h + [0, 8).
     V8 bq[D / 16];
 #pragma unroll
-    for (int k = 0; k < D / 16; ++k) bq[k] = nq[k];
-    if (g0 + 4 * 32 < c.n) fetch(g0 + 4 * 32);
+    for (int k = 0; k < D / 16; ++k) bq[k] = ld16<V8>(&rw[col * KS + 16 * k + 8 * h]);
+    if (g0 + 4 * 32 < c.n) fetch(noff);
+    cr = nr;
+    chd = nhd;
+    csl = nsl;
+    load_idx(g0 + 8 * 32, nr, nhd, nsl);
 
     floatx16_t s[KT];
 #pragma unroll
@@ -199,21 +235,57 @@ attend_mfma_kernel(AttnArgs a) {
         o[dt] = M::mma(ld16<V8>(&Vt[(dt * 32 + col) * VS + 16 * j + 8 * h]), bp, o[dt]);
     }
 
-    if (live) {
-      const int64_t dst = part_row(a, c, row, head) * a.slots + slot;
-      if (h == 0) {
-        a.part_m[dst] = m;
-        a.part_l[dst] = l;
-      }
-      // o[dt][v] is feature 32dt + 8(v/4) + 4h + v%4 of this lane's query:
-      // four consecutive features per (dt, v/4).
-      A* base = acc_out + dst * D + 4 * h;
+    const int64_t dst = live ? part_row(a, c, row, head) * a.slots + slot : -1;
+    const bool more = g0 + 4 * 32 < c.n;
+    // o[dt][v] is feature 32dt + 8(v/4) + 4h + v%4 of this lane's query.
+    // Stores go out after the next group's rows are staged, so the wait for
+    // those rows never includes them.
+    if constexpr (kWide) {
+      // Through LDS: four consecutive features per (dt, v/4) into the row of
+      // this lane's query, then whole rows out.
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
-          store4<A>(base + dt * 32 + 8 * q4, o[dt][4 * q4], o[dt][4 * q4 + 1],
-                    o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+          store4<A>(reinterpret_cast<A*>(&rw[col * KS + dt * 32 + 8 * q4 + 4 * h]),
+                    o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      u32x4 ov[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        ov[u] = *reinterpret_cast<const u32x4*>(&rw[(lane / RQ + (64 / RQ) * u) * KS + (lane % RQ) * 8]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (more) stage_q();
+      noff = q_off(nr, nhd, nsl);  // waits for the index loads, before any store
+      if (live && h == 0) {
+        a.part_m[dst] = m;
+        a.part_l[dst] = l;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int64_t rd = __shfl(dst, lane / RQ + (64 / RQ) * u);
+        if (rd >= 0) *reinterpret_cast<u32x4*>(acc_out + rd * D + (lane % RQ) * 8) = ov[u];
+      }
+    } else {
+      if (more) stage_q();
+      noff = q_off(nr, nhd, nsl);
+      if (live) {
+        if (h == 0) {
+          a.part_m[dst] = m;
+          a.part_l[dst] = l;
+        }
+        A* base = acc_out + dst * D + 4 * h;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            store4<A>(base + dt * 32 + 8 * q4, o[dt][4 * q4], o[dt][4 * q4 + 1],
+                      o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+      }
     }
   }
 }
