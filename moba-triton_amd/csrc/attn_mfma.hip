@@ -404,86 +404,102 @@ bwd_mfma_kernel(AttnArgs a) {
   for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
   A* dq_out = static_cast<A*>(a.part_acc);
 
-  // The next step's entry metadata and Q / dO rows are fetched into
-  // registers while the current step is computed, then written to LDS.
-  constexpr int CH = (NQ * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per tensor
-  constexpr int MT = (NQ + NT - 1) / NT;          // metadata entries per thread
-  uint4 pq[CH], po[CH];
-  int p_lim[MT];
-  float p_lse[MT], p_dl[MT];
-  int64_t p_dst[MT];
-  auto fetch = [&](int32_t g0) {
-#pragma unroll
-    for (int u = 0; u < MT; ++u) {
-      const int qi = tid + u * NT;
-      const int32_t e = g0 + qi;
-      p_lim[u] = -1; p_lse[u] = 0.f; p_dl[u] = 0.f; p_dst[u] = -1;
-      if (qi < NQ && e < c.n) {
-        const int32_t row = a.row_indices[c.lo + e];
-        const int32_t head = a.head_indices[c.lo + e];
-        const int32_t slot = a.slot_of_pair[c.lo + e];
-        const int64_t pr = part_row(a, c, row, head);
-        p_lse[u] = a.lse[pr];
-        p_dl[u] = a.delta[pr];
-        p_dst[u] = pr * a.slots + slot;
-        const int64_t rrel = static_cast<int64_t>(row) - c.key0;
-        const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
-        p_lim[u] = min(key_lim - 1, row_lim);
-      }
-    }
+  // Entry pipeline. Every thread tracks entry tid % NQ of a step (lanes past
+  // NQ duplicate it), so all global loads are unconditional and the wait
+  // counts stay static: while step g is computed, the Q / dO rows and
+  // lse / delta of step g + 1 and the index entries of step g + 2 are in
+  // flight; everything is waited for once, before the step's stores.
+  constexpr int CH = NQ * D / 8 / NT;  // 16-byte chunks per thread per tensor
+  static_assert(NQ * D / 8 % NT == 0, "row chunks must tile the workgroup");
+  const int qi = tid % NQ;
+  const int32_t last = c.n > 0 ? c.n - 1 : 0;
+  int32_t i_row = 0, i_head = 0, i_slot = -1;   // raw entry, step g + 2
+  auto load_idx = [&](int32_t g) {
+    const int32_t e = g + qi;
+    const int64_t i = c.lo + (e < c.n ? e : last);
+    i_row = a.row_indices[i];
+    i_head = a.head_indices[i];
+    i_slot = e < c.n ? a.slot_of_pair[i] : -1;
+  };
+  int64_t n_pr = 0, n_dst = -1;                 // derived, step g + 1
+  int n_lim = -1;
+  __shared__ int64_t s_qoff[NQ];
+  auto derive = [&]() {
+    const bool ok = i_slot >= 0;
+    const int64_t pr = part_row(a, c, i_row, i_head);
+    const int64_t rrel = static_cast<int64_t>(i_row) - c.key0;
+    const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
+    n_pr = ok ? pr : 0;
+    n_dst = ok ? pr * a.slots + i_slot : -1;
+    n_lim = ok ? min(key_lim - 1, row_lim) : -1;
+    if (tid < NQ) s_qoff[tid] = ok ? q_offset(a, c, i_row, i_head) : -1;
+  };
+  u32x4 pq[CH], po[CH];
+  bool pv[CH];  // chunk belongs to a live entry (zeroed when staged)
+  float n_lse = 0.f, n_dl = 0.f;
+  auto fetch = [&]() {  // step g + 1: rows via s_qoff, lse / delta via n_pr
+    n_lse = a.lse[n_pr];
+    n_dl = a.delta[n_pr];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = tid + u * NT;
-      pq[u] = make_uint4(0, 0, 0, 0);
-      po[u] = make_uint4(0, 0, 0, 0);
-      if (i < NQ * D / 8) {
-        const int32_t e = g0 + i / (D / 8);
-        if (e < c.n) {
-          const int32_t row = a.row_indices[c.lo + e];
-          const int32_t head = a.head_indices[c.lo + e];
-          const int64_t off = q_offset(a, c, row, head) + (i % (D / 8)) * 8;
-          pq[u] = *reinterpret_cast<const uint4*>(Qg + off);
-          po[u] = *reinterpret_cast<const uint4*>(Og + off);
-        }
-      }
+      const int64_t o = s_qoff[i / (D / 8)];
+      const int64_t off = (o >= 0 ? o : 0) + (i % (D / 8)) * 8;
+      pq[u] = *reinterpret_cast<const u32x4*>(Qg + off);
+      po[u] = *reinterpret_cast<const u32x4*>(Og + off);
+      pv[u] = o >= 0;
     }
   };
-  fetch(0);
+  int c_lim = -1;
+  int64_t c_dst = -1;
+  float c_lse = 0.f, c_dl = 0.f;
+  if (c.n > 0) {
+    load_idx(0);
+    derive();
+    __syncthreads();
+    fetch();
+    load_idx(NQ);
+    c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
+    derive();  // s_qoff now describes step 1; every thread read step 0's above
+  }
+  // vmcnt(0): the K / V operands and the prologue loads are all resident, so
+  // the loop's wait counts start from an empty queue on every path.
+  __builtin_amdgcn_s_waitcnt(0x0f70);
 
   for (int32_t g0 = 0; g0 < c.n; g0 += NQ) {
-    __syncthreads();  // previous step fully consumed (and K / V staged)
-#pragma unroll
-    for (int u = 0; u < MT; ++u) {
-      const int qi = tid + u * NT;
-      if (qi < NQ) {
-        s_lim[qi] = p_lim[u];
-        s_lse[qi] = p_lse[u];
-        s_delta[qi] = p_dl[u];
-        s_dst[qi] = p_dst[u];
-      }
+    __syncthreads();  // previous step fully consumed; s_qoff of step g + 1 visible
+    if (tid < NQ) {
+      s_lim[tid] = c_lim;
+      s_lse[tid] = c_lse;
+      s_delta[tid] = c_dl;
+      s_dst[tid] = c_dst;
     }
     // Q and dO rows: row-major and transposed (q permuted per 16-slice so
     // each lane-half's eight queries of a K-step are contiguous).
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = tid + u * NT;
-      if (i < NQ * D / 8) {
-        const int q = i / (D / 8);
-        const int d8 = (i % (D / 8)) * 8;
-        *reinterpret_cast<uint4*>(&Qs[q * RS + d8]) = pq[u];
-        *reinterpret_cast<uint4*>(&Os[q * RS + d8]) = po[u];
-        const uint16_t* qe = reinterpret_cast<const uint16_t*>(&pq[u]);
-        const uint16_t* oe = reinterpret_cast<const uint16_t*>(&po[u]);
-        const int qp = (q & ~15) + perm16(q & 15);
+      const int q = i / (D / 8);
+      const int d8 = (i % (D / 8)) * 8;
+      const u32x4 vq = pv[u] ? pq[u] : u32x4{0, 0, 0, 0};
+      const u32x4 vo = pv[u] ? po[u] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = vq;
+      *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = vo;
+      const uint16_t* qe = reinterpret_cast<const uint16_t*>(&vq);
+      const uint16_t* oe = reinterpret_cast<const uint16_t*>(&vo);
+      const int qp = (q & ~15) + perm16(q & 15);
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          Qt[(d8 + w) * QTS + qp] = qe[w];
-          Ot[(d8 + w) * QTS + qp] = oe[w];
-        }
+      for (int w = 0; w < 8; ++w) {
+        Qt[(d8 + w) * QTS + qp] = qe[w];
+        Ot[(d8 + w) * QTS + qp] = oe[w];
       }
     }
     __syncthreads();
-    if (g0 + NQ < c.n) fetch(g0 + NQ);
+    const bool more = g0 + NQ < c.n;
+    if (more) {
+      fetch();
+      load_idx(g0 + 2 * NQ);
+    }
 
     // S and dP for this wave's 32 keys and each 32-query tile; lane <->
     // key, register v <-> query 32 qt + 8(v/4) + 4h + v%4.
@@ -518,24 +534,67 @@ bwd_mfma_kernel(AttnArgs a) {
         }
       }
     }
-    __syncthreads();  // dS of every wave visible
+    __syncthreads();  // dS of every wave visible; Qs / Os free
 
     // dQ^T[d][q] over all BS keys; (feature tile, query tile) pairs spread
     // over the waves.
-    for (int tt = wave; tt < DT * QT; tt += NW) {
+    constexpr int TPW = DT * QT / NW;
+    static_assert(DT * QT % NW == 0, "dQ tiles must spread evenly over the waves");
+    floatx16_t dq[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tt = wave + t * NW;
       const int dt = tt % DT, qt = tt / DT;
-      floatx16_t dq = floatx16_t{};
+      dq[t] = floatx16_t{};
 #pragma unroll
       for (int j = 0; j < BS / 16; ++j)
-        dq = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
-                    ld16<V8>(&DS[(qt * 32 + col) * KTS + 16 * j + 8 * h]), dq);
-      const int64_t dst = s_dst[qt * 32 + col];
-      if (dst >= 0) {
-        A* base = dq_out + dst * D + dt * 32 + 4 * h;
+        dq[t] = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
+                       ld16<V8>(&DS[(qt * 32 + col) * KTS + 16 * j + 8 * h]), dq[t]);
+    }
+    // dq[t][v] is feature 32dt + 8(v/4) + 4h + v%4 of query 32qt + col.
+    if constexpr (sizeof(A) == 2) {
+      // Rows of dQ through LDS (Qs), then whole 16-byte chunks out.
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int tt = wave + t * NW;
+        const int dt = tt % DT, qt = tt / DT;
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
-          store4<A>(base + 8 * q4, dq[4 * q4] * a.scale, dq[4 * q4 + 1] * a.scale,
-                    dq[4 * q4 + 2] * a.scale, dq[4 * q4 + 3] * a.scale);
+          store4<A>(reinterpret_cast<A*>(&Qs[(qt * 32 + col) * RS + dt * 32 + 8 * q4 + 4 * h]),
+                    dq[t][4 * q4] * a.scale, dq[t][4 * q4 + 1] * a.scale,
+                    dq[t][4 * q4 + 2] * a.scale, dq[t][4 * q4 + 3] * a.scale);
+      }
+      __syncthreads();
+      if (more) {
+        c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
+        derive();  // waits for every load in flight, before the stores
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int i = tid + u * NT;
+        const int q = i / (D / 8);
+        const int d8 = (i % (D / 8)) * 8;
+        const int64_t dst = s_dst[q];
+        const u32x4 val = *reinterpret_cast<const u32x4*>(&Qs[q * RS + d8]);
+        if (dst >= 0) *reinterpret_cast<u32x4*>(dq_out + dst * D + d8) = val;
+      }
+    } else {
+      if (more) {
+        c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
+        derive();
+      }
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int tt = wave + t * NW;
+        const int dt = tt % DT, qt = tt / DT;
+        const int64_t dst = s_dst[qt * 32 + col];
+        if (dst >= 0) {
+          A* base = dq_out + dst * D + dt * 32 + 4 * h;
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            store4<A>(base + 8 * q4, dq[t][4 * q4] * a.scale, dq[t][4 * q4 + 1] * a.scale,
+                      dq[t][4 * q4 + 2] * a.scale, dq[t][4 * q4 + 3] * a.scale);
+        }
       }
     }
   }
