@@ -353,14 +353,22 @@ bwd_mfma_kernel(AttnArgs a) {
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
   constexpr int KTS = BS + 8;   // row stride of K^T and dS ([*][key])
   constexpr int QTS = NQ + 8;   // row stride of Q^T / dO^T ([d][q])
+  // Element (feature d, permuted query position qp) of Q^T / dO^T. The
+  // 8-element chunks of a row are XOR-swizzled by d / 8, so the transposing
+  // writes of one query's eight features (rows d8 .. d8 + 7 for every d8)
+  // fall into distinct banks; 8-aligned runs stay contiguous for the reads.
+  auto tq = [](int d, int qp) {
+    return d * QTS + ((((qp >> 3) ^ ((d >> 3) % (NQ / 8))) << 3) | (qp & 7));
+  };
   __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
   __shared__ __attribute__((aligned(16))) uint16_t Qs[NQ * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Os[NQ * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Qt[D * QTS];
   __shared__ __attribute__((aligned(16))) uint16_t Ot[D * QTS];
   __shared__ __attribute__((aligned(16))) uint16_t DS[NQ * KTS];
-  __shared__ float s_lse[NQ], s_delta[NQ];
-  __shared__ int s_lim[NQ];
+  __shared__ __attribute__((aligned(16))) float s_lse[NQ];
+  __shared__ __attribute__((aligned(16))) float s_delta[NQ];
+  __shared__ __attribute__((aligned(16))) int s_lim[NQ];
   __shared__ int64_t s_dst[NQ];
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
@@ -490,8 +498,8 @@ bwd_mfma_kernel(AttnArgs a) {
       const int qp = (q & ~15) + perm16(q & 15);
 #pragma unroll
       for (int w = 0; w < 8; ++w) {
-        Qt[(d8 + w) * QTS + qp] = qe[w];
-        Ot[(d8 + w) * QTS + qp] = oe[w];
+        Qt[tq(d8 + w, qp)] = qe[w];
+        Ot[tq(d8 + w, qp)] = oe[w];
       }
     }
     __syncthreads();
@@ -515,22 +523,33 @@ bwd_mfma_kernel(AttnArgs a) {
       }
       V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int q = qt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        const bool ok = mykey <= s_lim[q];
-        const float p = ok ? __builtin_amdgcn_exp2f(sacc[v] * a.scale_log2 - s_lse[q]) : 0.f;
-        const float ds = p * (pacc[v] - s_delta[q]);
-        pb[v >> 3][v & 7] = static_cast<Sc>(p);
-        db[v >> 3][v & 7] = static_cast<Sc>(ds);
-        DS[q * KTS + mykey] = __builtin_bit_cast(uint16_t, static_cast<Sc>(ds));
+      for (int g = 0; g < 4; ++g) {  // queries 32qt + 8g + 4h + [0, 4)
+        const int q0 = qt * 32 + 8 * g + 4 * h;
+        const int4 lim4 = *reinterpret_cast<const int4*>(&s_lim[q0]);
+        const float4 lse4 = *reinterpret_cast<const float4*>(&s_lse[q0]);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&s_delta[q0]);
+        const int limv[4] = {lim4.x, lim4.y, lim4.z, lim4.w};
+        const float lsev[4] = {lse4.x, lse4.y, lse4.z, lse4.w};
+        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int v = 4 * g + w;
+          const int q = q0 + w;
+          const float x = mykey <= limv[w] ? sacc[v] * a.scale_log2 - lsev[w] : -INFINITY;
+          const float p = __builtin_amdgcn_exp2f(x);
+          const float ds = p * (pacc[v] - dlv[w]);
+          pb[v >> 3][v & 7] = static_cast<Sc>(p);
+          db[v >> 3][v & 7] = static_cast<Sc>(ds);
+          DS[q * KTS + mykey] = __builtin_bit_cast(uint16_t, static_cast<Sc>(ds));
+        }
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int qoff = qt * 32 + 16 * j + 8 * h;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          dv[dt] = M::mma(ld16<V8>(&Ot[(dt * 32 + col) * QTS + qoff]), pb[j], dv[dt]);
-          dk[dt] = M::mma(ld16<V8>(&Qt[(dt * 32 + col) * QTS + qoff]), db[j], dk[dt]);
+          dv[dt] = M::mma(ld16<V8>(&Ot[tq(dt * 32 + col, qoff)]), pb[j], dv[dt]);
+          dk[dt] = M::mma(ld16<V8>(&Qt[tq(dt * 32 + col, qoff)]), db[j], dk[dt]);
         }
       }
     }
