@@ -36,6 +36,7 @@ namespace moba {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte chunk
 
 // Workspace layout (bytes): [0, 256) counter; [256, 256 + 4*R*Hkv) norms
 // rounded up to 256; then the queue of query ids (int64 each).
@@ -138,22 +139,6 @@ __device__ inline void insert_exact(float (&val)[M], int (&idx)[M], float s, int
       s = tv; j = ti;
       carry = true;
     }
-  }
-}
-
-// Branch-free insertion into a list sorted by value only (approximate scores;
-// ties among them are settled later by the exact rescoring).
-template <int M>
-__device__ inline void insert_approx(float (&val)[M], int (&idx)[M], float s, int j) {
-#pragma unroll
-  for (int p = 0; p < M; ++p) {
-    const bool gt = s > val[p];
-    const float nv = gt ? s : val[p];
-    const int ni = gt ? j : idx[p];
-    s = gt ? val[p] : s;
-    j = gt ? idx[p] : j;
-    val[p] = nv;
-    idx[p] = ni;
   }
 }
 
@@ -377,6 +362,58 @@ __device__ inline V load_vec16(const void* p) {
   return __builtin_bit_cast(V, u);
 }
 
+// Approximate-score keys. A key is the float32 approximate score with its
+// low 16 mantissa bits replaced by the block id, read through the
+// order-preserving map float bits <-> signed int (an involution), so that
+// integer max / min / med3 order keys by score, and the id rides along.
+// |value(key) - score| < 2^-7 |value(key)| (1 + 2^-7) for normal scores, and
+// below 2^-133 in the subnormal range.
+__device__ inline int ord_map(uint32_t bits) {
+  return static_cast<int>(bits ^ (static_cast<uint32_t>(static_cast<int>(bits) >> 31) >> 1));
+}
+__device__ inline float key_value(int k) { return u2f(static_cast<uint32_t>(ord_map(static_cast<uint32_t>(k)))); }
+__device__ inline int key_id(int k) { return ord_map(static_cast<uint32_t>(k)) & 0xffff; }
+constexpr int kNoKey = -2147483647 - 1;  // below every key (no entry)
+
+__device__ inline int med3i(int a, int b, int c) {
+  int d;
+  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+// Inserts x into a list sorted descending; the smallest entry falls off.
+// New entry p is the median of old entries p - 1, p and x.
+template <int M>
+__device__ inline void insert_key(int (&l)[M], int x) {
+#pragma unroll
+  for (int p = M - 1; p > 0; --p) l[p] = med3i(l[p - 1], l[p], x);
+  l[0] = max(l[0], x);
+}
+// Same for floats (values only).
+template <int K>
+__device__ inline void insert_value(float (&l)[K], float x) {
+#pragma unroll
+  for (int p = K - 1; p > 0; --p) l[p] = __builtin_amdgcn_fmed3f(l[p - 1], l[p], x);
+  l[0] = fmaxf(l[0], x);
+}
+// k-th largest key (1-based, k <= M) of the union of two descending lists
+// of distinct keys; kNoKey when the union holds fewer than k keys.
+template <int M>
+__device__ inline int kth_key(const int (&A)[M], const int (&B)[M], int k) {
+  int best = kNoKey;
+#pragma unroll
+  for (int i = 0; i <= M; ++i) {
+    if (i > k) break;
+    const int a = i == 0 ? 0x7fffffff : A[i - 1];
+    const int jb = k - i;
+    int b = 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < M; ++u) b = (u == jb - 1) ? B[u] : b;
+    if (jb > M) b = kNoKey;
+    best = max(best, min(a, b));
+  }
+  return best;
+}
+
 template <typename T, int D, int M, int K, int CAP, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64)
 gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
@@ -391,8 +428,8 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   constexpr int KROW = D + 8;                      // staged kbar row stride (elements)
   constexpr int NT = WAVES * 64;
   constexpr int KCH = (32 * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per stage
-  __shared__ float s_val[WAVES][CAP][64];
-  __shared__ uint16_t s_idx[WAVES][CAP][64];
+  constexpr float kTr = 0.0078125f * 1.01f;        // key truncation, relative
+  __shared__ uint32_t s_buf[WAVES][CAP][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_kb[2][32 * KROW];
 
   const int tid = threadIdx.x;
@@ -445,19 +482,28 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   const float qnorm = sqrtf(qn) * 1.0001f;
   const float knorm = kbar_norm[r * h_kv + hk];
   const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
+  // Decision band around a key value x: two scores whose keys lie more than
+  // band(x) apart (magnitudes <= band_mag(x)) round to distinct values of
+  // the storage dtype, in key order. band_mag also covers the magnitude of
+  // x - band(x) itself.
+  auto band_mag = [&](float x) { return (fabsf(x) + 2.f * E) * 1.05f + 2.f * Ops::kGapAbs; };
+  auto band_at = [&](float m) {
+    return 2.f * E + 2.f * kTr * m + Ops::kGapRel * (m + E) + Ops::kGapAbs;
+  };
+  auto band = [&](float x) { return band_at(band_mag(x)); };
 
   const int n_chunks = (take > 0 && hz > 0) ? (hz + 31) / 32 : 0;
   // kbar chunks of 32 rows are staged in LDS by the whole workgroup. Rows
   // past the horizon are clamped to a valid row; their scores are masked
   // (every such block is >= own for every query here).
-  uint4 kreg[KCH];
+  u32x4 kreg[KCH];
   auto kload = [&](int ch) {
 #pragma unroll
     for (int u = 0; u < KCH; ++u) {
       const int i = tid + u * NT;
       if (i < 32 * D / 8) {
         const int blk = min(ch * 32 + i / (D / 8), hz - 1);
-        kreg[u] = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(blk) * D +
+        kreg[u] = *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(blk) * D +
                                                  (i % (D / 8)) * 8);
       }
     }
@@ -467,7 +513,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     for (int u = 0; u < KCH; ++u) {
       const int i = tid + u * NT;
       if (i < 32 * D / 8)
-        *reinterpret_cast<uint4*>(&s_kb[buf][(i / (D / 8)) * KROW + (i % (D / 8)) * 8]) =
+        *reinterpret_cast<u32x4*>(&s_kb[buf][(i / (D / 8)) * KROW + (i % (D / 8)) * 8]) =
             kreg[u];
     }
   };
@@ -502,13 +548,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        float x = (full || b < own) ? acc[v] : -INFINITY;
-#pragma unroll
-        for (int p = 0; p < K; ++p) {
-          const float hi = fmaxf(tk[p], x);
-          x = fminf(tk[p], x);
-          tk[p] = hi;
-        }
+        insert_value<K>(tk, (full || b < own) ? acc[v] : -INFINITY);
       }
       __syncthreads();
     }
@@ -516,113 +556,125 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
     for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
     const float tau = kth_of_union<K>(tk, pk, take);
-    if (tau > -INFINITY) theta = tau - 2.f * E - (Ops::kGapRel * (fabsf(tau) + E) + Ops::kGapAbs);
+    // The cut below is L's key minus band(L); the key may sit up to
+    // kTr |L| under the score, so theta carries that much more slack.
+    if (tau > -INFINITY) theta = tau - band(tau) - 2.f * kTr * band_mag(tau);
   }
   // Collection threshold: a > thr0 is a >= theta.
   const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
-  // --- Pass 2: every chunk; candidates >= theta that can still enter the
-  // lane's sorted list of the M best are appended to its LDS buffer, and a
-  // buffer about to overflow is folded into the list (the threshold then
-  // rises to the list's M-th best). Chunk ch + 1 waits in registers while
-  // ch is scored; ch + 2 is requested once ch + 1 is in LDS.
-  float lv[M];
-  int li[M];
+  // --- Pass 2: every chunk. Each score above the lane's threshold becomes
+  // a key in the lane's LDS buffer (written unconditionally, kept by
+  // advancing the count); a buffer that may overflow on the next chunk is
+  // folded into the lane's sorted list of its M best keys, and the
+  // threshold rises to the M-th. Chunk ch + 1 waits in registers while ch
+  // is scored; ch + 2 is requested once ch + 1 is in LDS.
+  int lk[M];
 #pragma unroll
-  for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
+  for (int p = 0; p < M; ++p) lk[p] = kNoKey;
+  uint32_t* sb = &s_buf[wave][0][lane];  // this lane's column of the buffer
   if (n_chunks > 0) {
     float thr = thr0;
     int cnt = 0;
+    auto fold = [&]() {
+      for (int e = 0; e < cnt; ++e) insert_key<M>(lk, ord_map(sb[e * 64]));
+      cnt = 0;
+      if (lk[M - 1] != kNoKey) thr = fmaxf(thr0, key_value(lk[M - 1]));
+    };
     kload(0);
     kstore(0);
     if (n_chunks > 1) kload(1);
     __syncthreads();
     for (int ch = 0; ch < n_chunks; ++ch) {
       const floatx16_t acc = score_chunk(ch & 1);
+      const uint32_t base = static_cast<uint32_t>(ch * 32 + 4 * half);
       if (ch * 32 + 32 <= own_min) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          if (acc[v] > thr) {
-            s_val[wave][cnt][lane] = acc[v];
-            s_idx[wave][cnt][lane] =
-                static_cast<uint16_t>(ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3));
-            ++cnt;
-          }
+          const uint32_t id = base + 8 * (v >> 2) + (v & 3);
+          sb[cnt * 64] = (f2u(acc[v]) & 0xffff0000u) | id;
+          cnt += acc[v] > thr ? 1 : 0;
         }
       } else {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-          const float a = (b < own) ? acc[v] : -INFINITY;
-          if (a > thr) {
-            s_val[wave][cnt][lane] = a;
-            s_idx[wave][cnt][lane] = static_cast<uint16_t>(b);
-            ++cnt;
-          }
+          const uint32_t id = base + 8 * (v >> 2) + (v & 3);
+          const float a = static_cast<int>(id) < own ? acc[v] : -INFINITY;
+          sb[cnt * 64] = (f2u(a) & 0xffff0000u) | id;
+          cnt += a > thr ? 1 : 0;
         }
       }
-      if (__any(cnt > CAP - 16)) {
-        for (int e = 0; e < cnt; ++e) {
-          const float sv = s_val[wave][e][lane];
-          if (sv > lv[M - 1]) insert_approx<M>(lv, li, sv, s_idx[wave][e][lane]);
-        }
-        cnt = 0;
-        thr = fmaxf(thr0, lv[M - 1]);
-      }
+      if (__any(cnt > CAP - 16)) fold();
       if (ch + 1 < n_chunks) kstore((ch + 1) & 1);
       if (ch + 2 < n_chunks) kload(ch + 2);
       __syncthreads();
     }
-    for (int e = 0; e < cnt; ++e) {
-      const float sv = s_val[wave][e][lane];
-      if (sv > lv[M - 1]) insert_approx<M>(lv, li, sv, s_idx[wave][e][lane]);
-    }
+    fold();
   }
   int n_in_list = 0;
 #pragma unroll
-  for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
+  for (int p = 0; p < M; ++p) n_in_list += lk[p] != kNoKey ? 1 : 0;
 
   // --- Merge the two half-lists of this query and decide. -----------------
-  // Candidates >= theta left out of a lane's list are <= its M-th best (and
-  // there are none while the list is not full); candidates below theta are
-  // checked against the final cut below.
-  const float rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
-  const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
-  float pv[M];
-  int pi[M];
+  // Every key k carries |value(k) - exact| <= E + kTr |value(k)|. Scores
+  // >= theta left out of a lane's list are <= its M-th key (rej; none while
+  // the list is not full); scores below theta never entered.
+  const int rej_mine = (n_in_list == M) ? lk[M - 1] : kNoKey;
+  const int rejk = max(rej_mine, __shfl_xor(rej_mine, 32));
+  int pk[M];
 #pragma unroll
-  for (int p = 0; p < M; ++p) {
-    pv[p] = __shfl_xor(lv[p], 32);
-    pi[p] = __shfl_xor(li[p], 32);
-  }
-  // L = the take-th largest approximate score of the union.
-  const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
+  for (int p = 0; p < M; ++p) pk[p] = __shfl_xor(lk[p], 32);
+  // L: the take-th key of the union; N: the (take + 1)-th.
+  const int Lk = take > 0 ? kth_key<M>(lk, pk, take) : kNoKey;
+  const int Nk = take > 0 ? kth_key<M>(lk, pk, take + 1) : kNoKey;
+  const float Lf = Lk != kNoKey ? key_value(Lk) : -INFINITY;
+  const float Nf = Nk != kNoKey ? key_value(Nk) : -INFINITY;
+  const float rejf = rejk != kNoKey ? key_value(rejk) : -INFINITY;
   bool ok = true;
   float cut = -INFINITY;
-  if (take > 0 && L > -INFINITY) {
-    const float mag = fmaxf(fabsf(L), fabsf(rej == -INFINITY ? 0.f : rej)) + E;
-    const float gap = Ops::kGapRel * mag + Ops::kGapAbs;
+  if (take > 0 && Lf > -INFINITY) {
+    const float mag = band_mag(Lf);
     if (!(mag < Ops::kMaxFinite)) ok = false;
-    if (rej > -INFINITY && !(L - rej > 2.f * E + gap)) ok = false;
-    cut = L - 2.f * E - gap;
+    if (rejf > -INFINITY &&
+        !(Lf - rejf > band_at(fmaxf(mag, band_mag(rejf))))) ok = false;
+    cut = Lf - band_at(mag);
     if (!(cut >= theta)) ok = false;  // a needed candidate may lie below theta
   }
-  if (take > 0 && !(E < INFINITY)) ok = false;  // q or kbar carries inf / NaN
-  // Exact rescoring of every union entry within the band, by the two lanes
-  // together: each forms the exact (float64) partial dot over the features
-  // it holds, and the partials are added. Both lanes walk the union in the
-  // same order (half 0's list first) and keep identical exact lists.
+  // q or kbar carries inf / NaN, or a float32 score could overflow.
+  if (take > 0 && !(qnorm * knorm < 3.0e38f)) ok = false;
+  // Union entries >= cut: those that surely outrank the (take + 1)-th key
+  // (and so everything from there down) are selected outright; the rest
+  // are rescored exactly (float64) by the two lanes together, each forming
+  // the partial dot over the features it holds. Both lanes walk the union
+  // in the same order (half 0's list first) and keep identical lists, in
+  // which an outright selection ranks first (score +inf, then by id).
   float fv[M];
   int fi[M];
 #pragma unroll
   for (int p = 0; p < M; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
   if (ok && take > 0 && live) {
+    const float hiN = Nk != kNoKey ? Nf + kTr * fabsf(Nf) + E : -INFINITY;
+    // The union in walk order, through the (now idle) buffer: 2M <= CAP.
 #pragma unroll
+    for (int p = 0; p < M; ++p) {
+      sb[p * 64] = static_cast<uint32_t>(half == 0 ? lk[p] : pk[p]);
+      sb[(M + p) * 64] = static_cast<uint32_t>(half == 0 ? pk[p] : lk[p]);
+    }
+#pragma unroll 1
     for (int p = 0; p < 2 * M; ++p) {
-      const bool first = (p < M) == (half == 0);
-      const float a = first ? (p < M ? lv[p] : lv[p - M]) : (p < M ? pv[p] : pv[p - M]);
-      const int j = first ? (p < M ? li[p] : li[p - M]) : (p < M ? pi[p] : pi[p - M]);
-      if (a > -INFINITY && a >= cut) {
+      const int k = static_cast<int>(sb[p * 64]);
+      if (k == kNoKey) continue;
+      const float x = key_value(k);
+      if (!(x >= cut)) continue;
+      const int j = key_id(k);
+      bool sure = Nk == kNoKey;
+      if (!sure) {
+        const float lo = x - kTr * fabsf(x) - E;
+        const float mi = fmaxf(fabsf(x) * (1.f + kTr) + E, fabsf(hiN));
+        sure = lo - hiN > Ops::kGapRel * mi + Ops::kGapAbs;
+      }
+      float sc = INFINITY;
+      if (!sure) {
         const T* krow = kb + static_cast<int64_t>(j) * D + 8 * half;
         double part = 0.0;
 #pragma unroll
@@ -634,9 +686,9 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                     static_cast<double>(static_cast<float>(kv[i]));
         }
         part += __shfl_xor(part, 32);
-        const float sc = Elem<T>::round(static_cast<float>(part));
-        if (sc > -INFINITY) insert_exact<M>(fv, fi, sc, j);
+        sc = Elem<T>::round(static_cast<float>(part));
       }
+      if (sc > -INFINITY) insert_exact<M>(fv, fi, sc, j);
     }
   }
   if (!live || half != 0) return;
