@@ -34,6 +34,16 @@ SWEEP = (65536, 131072, 262144, 524288)
 H100_FWD_MS = {65536: 1.492, 131072: 3.942, 262144: 11.609, 524288: 38.164}
 H100_FWDBWD_MS = {65536: 2.658, 131072: 6.181, 262144: 16.076, 524288: 47.046}
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+# HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs,
+# scaled by the same counters' reading for a plain copy of known size.
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_fwd_bwd_S524288.json"
+# Stage -> the kernel that dominates it (name as rocprofv3 reports it).
+STAGE_KERNEL = {
+    "pool": "pool_kernel", "gate": "gate_mfma_kernel", "csc": "tile_count_or_scatter_kernel",
+    "attend": "attend_mfma_kernel", "combine": "combine_kernel", "delta": "delta_kernel",
+    "bwd": "bwd_mfma_kernel", "dq_reduce": "dq_reduce_kernel",
+}
 
 
 def algorithmic_bytes(s, b=1, hq=HEADS, hkv=HEADS, d=HEAD_DIM, k=TOPK, e=2):
@@ -50,6 +60,16 @@ def algorithmic_bytes(s, b=1, hq=HEADS, hkv=HEADS, d=HEAD_DIM, k=TOPK, e=2):
         "bwd": 2 * k * n * d * e + 8 * k * n + 4 * nkv * d * e + k * n * d * e + 12 * n * k,
         "dq_reduce": k * n * d * e + 4 * n * k + n * d * e,
     }
+
+
+def gate_flops(s, hq=HEADS, d=HEAD_DIM, bs=BLOCK):
+    """MFMA work of the gate per call: one D-long dot per (query, strictly
+    past block) pair, padded to whole 32-block tiles as the kernel runs it."""
+    pairs = 0
+    for t0 in range(0, s, 128):       # 128 queries share one tile horizon
+        hz = min(t0 + 127, s - 1) // bs
+        pairs += 128 * ((hz + 31) // 32) * 32
+    return 2 * d * pairs * hq
 
 
 def make_inputs(s, dev, seed=0):
@@ -203,8 +223,18 @@ def main():
     ap.add_argument("--seq", type=int, default=524288)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=2048)
+    ap.add_argument("--cpu-rows", type=int, default=16384)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device copy (HBM counter calibration)")
     args = ap.parse_args()
+    if args.copy_probe:
+        x = torch.empty(1 << 29, dtype=torch.int16, device="cuda:0").fill_(1)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_each_way": x.numel() * x.element_size()}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested). Run with --gpus 1.", file=sys.stderr)
@@ -238,11 +268,35 @@ def main():
 
     stages = stage_times(s, dev)
     ab = algorithmic_bytes(s)
-    dom = max(stages, key=stages.get)
-    achieved = ab[dom] / (stages[dom] * 1e-3) / 1e9
-    stage_rows = {n: {"ms": round(t, 4), "alg_GBps": round(ab[n] / (t * 1e-3) / 1e9, 1)}
-                  for n, t in stages.items()}
+    gf = gate_flops(s)
+    stage_rows = {}
+    for n, t in stages.items():
+        row = {"ms": round(t, 4), "kernel": STAGE_KERNEL[n],
+               "alg_GBps": round(ab[n] / (t * 1e-3) / 1e9, 1),
+               "hbm_frac": round(ab[n] / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if n == "gate":
+            row["mfma_TFLOPs"] = round(gf / (t * 1e-3) / 1e12, 1)
+            row["mfma_frac"] = round(gf / (t * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+        stage_rows[n] = row
     print(f"[bench] stages {stage_rows}", file=sys.stderr, flush=True)
+    dom = max(stages, key=stages.get)
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        tr = json.loads(TRAFFIC_FILE.read_text()).get("kernels", {}).get(STAGE_KERNEL[dom])
+        if tr and tr.get("seq_len") == s:
+            traffic = tr["hbm_bytes_per_launch"]
+    if dom == "gate":
+        achieved = gf / (stages[dom] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": STAGE_KERNEL[dom], "achieved": round(achieved, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                "algorithmic": gf}
+    else:
+        achieved = ab[dom] / (stages[dom] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": STAGE_KERNEL[dom], "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "algorithmic": ab[dom]}
     total_alg = sum(ab.values())
     rows = [] if args.no_sweep else sweep(dev, SWEEP)
     cpu = None if args.no_cpu else cpu_baseline(s, args.cpu_rows)
@@ -258,9 +312,7 @@ def main():
         "config": {"workload": "moba_fwd_bwd", "batch": 1, "seq_len": s, "heads_q": HEADS,
                    "heads_kv": HEADS, "head_dim": HEAD_DIM, "block_size": BLOCK,
                    "top_k": TOPK, "causal": True},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": roof,
         "step_roofline": {"alg_bytes": total_alg,
                           "alg_GBps": round(total_alg / (ms * 1e-3) / 1e9, 1),
                           "frac": round(total_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},

@@ -60,7 +60,7 @@ const char* moba_status_string(int status);
  * to the input dtype. A short tail block divides by its real count.
  * k: [B, S, Hkv, D]; kbar: [R, Hkv, n_blocks, D]. Packed: blocks never
  * cross sequence boundaries and rows beyond a sequence's own block count are
- * left untouched.
+ * written as zeros.
  */
 int moba_pool(const void* k, void* kbar, const int32_t* cu_seqlens,
               int64_t batch, int64_t seq_len, int64_t max_seqlen,

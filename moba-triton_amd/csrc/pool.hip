@@ -23,7 +23,11 @@ pool_kernel(const T* __restrict__ k, T* __restrict__ kbar,
   const int64_t h = blockIdx.y % h_kv;
   const SeqSpan sp = seq_span(cu, r, S);
   const int64_t lo = blk * bs;
-  if (lo >= sp.len) return;  // a padded block slot of a short sequence
+  if (lo >= sp.len) {  // a padded block slot of a short sequence: zeros
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x)
+      Elem<T>::store(kbar, ((r * h_kv + h) * n_blocks + blk) * D + d, 0.f);
+    return;
+  }
   const int64_t hi = lo + bs < sp.len ? lo + bs : sp.len;
   for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
     double acc = 0.0;

@@ -143,16 +143,17 @@ def gate_scores(q: torch.Tensor, kbar: torch.Tensor,
     return out
 
 
-def select_from_scores(scores: torch.Tensor, cfg) -> torch.Tensor:
+def select_from_scores(scores: torch.Tensor, cfg, pos=None) -> torch.Tensor:
     """Selection mask `[B, H, S, n]` from gate scores, `naive.py:111-146`.
 
     Candidates are blocks strictly before the query's own block; a stable
     descending sort ranks them so equal scores favour the lower block index;
     the first `past_blocks_selected(n)` survive, -inf leftovers are dropped,
-    and the own block is OR-ed in when forced.
+    and the own block is OR-ed in when forced. `pos` gives the sequence
+    position of each score row (default: row r is position r).
     """
     b, h, s, n = scores.shape
-    pos = torch.arange(s)
+    pos = torch.arange(s) if pos is None else torch.as_tensor(pos, dtype=torch.int64)
     own = pos // cfg.block_size
     blocks = torch.arange(n)
     is_past = blocks.view(1, -1) < own.view(-1, 1)
@@ -172,6 +173,16 @@ def select_from_scores(scores: torch.Tensor, cfg) -> torch.Tensor:
 def gate_select(q: torch.Tensor, kbar: torch.Tensor, cfg) -> torch.Tensor:
     """`naive.py:64-146` with this oracle's score rounding."""
     return select_from_scores(gate_scores(q, kbar), cfg)
+
+
+def gate_select_rows(q: torch.Tensor, kbar: torch.Tensor, cfg, rows) -> torch.Tensor:
+    """`gate_select(q, kbar, cfg)[:, :, rows]` without scoring the other rows:
+    the selection of a query depends only on its own row and position, so the
+    same scores and ranking restricted to `rows` (positions in one sequence)
+    give the same mask `[B, H, len(rows), n]`. For full-length sequences where
+    the dense `[S, n]` score matrix would not fit."""
+    rows = torch.as_tensor(rows, dtype=torch.int64)
+    return select_from_scores(gate_scores(q[:, rows], kbar), cfg, pos=rows)
 
 
 def moba_selection(q, k, cfg, cu_seqlens=None) -> torch.Tensor:

@@ -203,3 +203,15 @@ def test_c_oracle_equals_torch_oracle(dt):
     assert torch.equal(c_oracle.pool_blocks(k, 64), kb)
     assert torch.equal(c_oracle.gate_select(q, kb, c),
                        O.mask_to_indices(O.gate_select(q, kb, c), 5))
+
+
+@pytest.mark.parametrize("s,bs,tk", [(2048, 64, 5), (1000, 32, 8)])
+def test_gate_rows_equal_the_full_gate_restricted(s, bs, tk):
+    """The row-subset gate (used at full sequence lengths) is the full gate
+    read at those rows, including the first rows, block edges and the tail."""
+    c = cfg(bs, tk)
+    q, k, _ = (t.to(torch.bfloat16) for t in qkv(2, s, 4, 64, dtype=torch.float32, seed=9))
+    kbar = O.pool_blocks(k, bs)
+    full = O.gate_select(q, kbar, c)
+    rows = torch.tensor(sorted({0, 1, bs - 1, bs, 3 * bs + 7, s // 2, s - 2, s - 1}))
+    assert torch.equal(O.gate_select_rows(q, kbar, c, rows), full[:, :, rows])
