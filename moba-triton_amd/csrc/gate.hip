@@ -415,7 +415,7 @@ __device__ inline int kth_key(const int (&A)[M], const int (&B)[M], int k) {
 }
 
 template <typename T, int D, int M, int K, int CAP, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64)
+__global__ void __launch_bounds__(WAVES * 64, (D == 64 && M <= 12) ? 3 : 1)
 gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                  int32_t* __restrict__ out, const int32_t* __restrict__ cu,
                  int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
@@ -496,25 +496,26 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // kbar chunks of 32 rows are staged in LDS by the whole workgroup. Rows
   // past the horizon are clamped to a valid row; their scores are masked
   // (every such block is >= own for every query here).
-  u32x4 kreg[KCH];
-  auto kload = [&](int ch) {
+  // Chunk ch's rows wait in register slot ch % 3 (loaded three chunks ahead)
+  // until they are stored to LDS buffer ch % 2.
+  u32x4 kr0[KCH], kr1[KCH], kr2[KCH];
+  auto kload = [&](u32x4 (&r)[KCH], int ch) {
 #pragma unroll
     for (int u = 0; u < KCH; ++u) {
       const int i = tid + u * NT;
       if (i < 32 * D / 8) {
         const int blk = min(ch * 32 + i / (D / 8), hz - 1);
-        kreg[u] = *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(blk) * D +
-                                                 (i % (D / 8)) * 8);
+        r[u] = *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(blk) * D +
+                                              (i % (D / 8)) * 8);
       }
     }
   };
-  auto kstore = [&](int buf) {
+  auto kstore = [&](const u32x4 (&r)[KCH], int buf) {
 #pragma unroll
     for (int u = 0; u < KCH; ++u) {
       const int i = tid + u * NT;
       if (i < 32 * D / 8)
-        *reinterpret_cast<u32x4*>(&s_kb[buf][(i / (D / 8)) * KROW + (i % (D / 8)) * 8]) =
-            kreg[u];
+        *reinterpret_cast<u32x4*>(&s_kb[buf][(i / (D / 8)) * KROW + (i % (D / 8)) * 8]) = r[u];
     }
   };
   auto score_chunk = [&](int buf) {
@@ -525,33 +526,56 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     return acc;  // acc[v] scores block 32 ch + 8(v/4) + 4 half + v%4
   };
 
-  // --- Pass 1: a lower bound on L from every fourth chunk. ---------------
-  // The take-th best of any subset of a query's candidates is <= the
-  // take-th best of all of them (L), so every candidate that can matter
-  // scores >= theta = (that value) - 2E - gap. Each lane keeps the K best of
-  // its half of the sample; the take-th best of the union of the two lists
-  // is the take-th best of a subset of the sample, so it bounds L as well.
+  // --- Pass 1: a lower bound on L from every chunk's maximum. ------------
+  // Each lane keeps the K largest of its per-chunk maxima (one score of one
+  // block each, all distinct blocks). The take-th largest of the union of
+  // the two lanes' lists is the take-th best of a subset of the query's
+  // candidates, so it is <= L (the take-th best of all of them); with the
+  // top blocks spread over chunks it is L itself. Every candidate that can
+  // matter then scores >= theta = (that value) - band - key slack.
   // Lane 0 of the wave holds its smallest query, so its own block bounds
   // every lane's: chunks entirely below it need no causal mask.
   const int own_min = __builtin_amdgcn_readfirstlane(own);
   float theta = -INFINITY;
+  auto stream_chunks = [&](auto&& body) {
+    // step(c): score chunk c, move chunk c + 1 from `next` into LDS, and
+    // request chunk c + 3 into the slot chunk c came from (`freed`).
+    auto step = [&](int c, const u32x4 (&next)[KCH], u32x4 (&freed)[KCH]) {
+      if (c >= n_chunks) return;
+      body(c, score_chunk(c & 1), c * 32 + 32 <= own_min);
+      if (c + 1 < n_chunks) kstore(next, (c + 1) & 1);
+      if (c + 3 < n_chunks) kload(freed, c + 3);
+      __syncthreads();
+    };
+    kload(kr0, 0);
+    if (n_chunks > 1) kload(kr1, 1);
+    if (n_chunks > 2) kload(kr2, 2);
+    kstore(kr0, 0);
+    __syncthreads();
+    for (int ch = 0; ch < n_chunks; ch += 3) {
+      step(ch, kr1, kr0);
+      step(ch + 1, kr2, kr1);
+      step(ch + 2, kr0, kr2);
+    }
+  };
   if (n_chunks > 0) {
     float tk[K];
 #pragma unroll
     for (int p = 0; p < K; ++p) tk[p] = -INFINITY;
-    for (int ch = 0; ch < n_chunks; ch += 4) {
-      kload(ch);
-      kstore(0);
-      __syncthreads();
-      const floatx16_t acc = score_chunk(0);
-      const bool full = ch * 32 + 32 <= own_min;
+    stream_chunks([&](int ch, const floatx16_t& acc, bool full) {
+      float mx = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        insert_value<K>(tk, (full || b < own) ? acc[v] : -INFINITY);
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[v]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+          mx = fmaxf(mx, b < own ? acc[v] : -INFINITY);
+        }
       }
-      __syncthreads();
-    }
+      insert_value<K>(tk, mx);
+    });
     float pk[K];
 #pragma unroll
     for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
@@ -563,12 +587,11 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Collection threshold: a > thr0 is a >= theta.
   const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
-  // --- Pass 2: every chunk. Each score above the lane's threshold becomes
-  // a key in the lane's LDS buffer (written unconditionally, kept by
-  // advancing the count); a buffer that may overflow on the next chunk is
+  // --- Pass 2: every chunk again. Each score above the lane's threshold
+  // (rare: theta sits within the decision band of L) becomes a key in the
+  // lane's LDS buffer; a buffer that may overflow on the next chunk is
   // folded into the lane's sorted list of its M best keys, and the
-  // threshold rises to the M-th. Chunk ch + 1 waits in registers while ch
-  // is scored; ch + 2 is requested once ch + 1 is in LDS.
+  // threshold rises to the M-th.
   int lk[M];
 #pragma unroll
   for (int p = 0; p < M; ++p) lk[p] = kNoKey;
@@ -581,34 +604,31 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       cnt = 0;
       if (lk[M - 1] != kNoKey) thr = fmaxf(thr0, key_value(lk[M - 1]));
     };
-    kload(0);
-    kstore(0);
-    if (n_chunks > 1) kload(1);
-    __syncthreads();
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      const floatx16_t acc = score_chunk(ch & 1);
-      const uint32_t base = static_cast<uint32_t>(ch * 32 + 4 * half);
-      if (ch * 32 + 32 <= own_min) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const uint32_t id = base + 8 * (v >> 2) + (v & 3);
-          sb[cnt * 64] = (f2u(acc[v]) & 0xffff0000u) | id;
-          cnt += acc[v] > thr ? 1 : 0;
+    // A score is appended only when it beats the threshold; the wave-wide
+    // ballot skips the append for the (common) scores no lane keeps.
+    auto append = [&](float a, uint32_t id) {
+      const bool hit = a > thr;
+      if (__ballot(hit) != 0) {
+        if (hit) {
+          sb[cnt * 64] = (f2u(a) & 0xffff0000u) | id;
+          ++cnt;
         }
+      }
+    };
+    stream_chunks([&](int ch, const floatx16_t& acc, bool full) {
+      const uint32_t base = static_cast<uint32_t>(ch * 32 + 4 * half);
+      if (full) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) append(acc[v], base + 8 * (v >> 2) + (v & 3));
       } else {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const uint32_t id = base + 8 * (v >> 2) + (v & 3);
-          const float a = static_cast<int>(id) < own ? acc[v] : -INFINITY;
-          sb[cnt * 64] = (f2u(a) & 0xffff0000u) | id;
-          cnt += a > thr ? 1 : 0;
+          append(static_cast<int>(id) < own ? acc[v] : -INFINITY, id);
         }
       }
       if (__any(cnt > CAP - 16)) fold();
-      if (ch + 1 < n_chunks) kstore((ch + 1) & 1);
-      if (ch + 2 < n_chunks) kload(ch + 2);
-      __syncthreads();
-    }
+    });
     fold();
   }
   int n_in_list = 0;
@@ -660,6 +680,9 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       sb[p * 64] = static_cast<uint32_t>(half == 0 ? lk[p] : pk[p]);
       sb[(M + p) * 64] = static_cast<uint32_t>(half == 0 ? pk[p] : lk[p]);
     }
+    // Classify; uncertain ids go back into the buffer (slot u <= p, already
+    // read), then are rescored R at a time so their row loads overlap.
+    int nu = 0;
 #pragma unroll 1
     for (int p = 0; p < 2 * M; ++p) {
       const int k = static_cast<int>(sb[p * 64]);
@@ -673,22 +696,38 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
         const float mi = fmaxf(fabsf(x) * (1.f + kTr) + E, fabsf(hiN));
         sure = lo - hiN > Ops::kGapRel * mi + Ops::kGapAbs;
       }
-      float sc = INFINITY;
-      if (!sure) {
-        const T* krow = kb + static_cast<int64_t>(j) * D + 8 * half;
+      if (sure) {
+        insert_exact<M>(fv, fi, INFINITY, j);
+      } else {
+        sb[nu * 64] = static_cast<uint32_t>(j);
+        ++nu;
+      }
+    }
+    constexpr int R = 2;
+#pragma unroll 1
+    for (int u0 = 0; u0 < nu; u0 += R) {
+      int jr[R];
+      V kv[R][KSTEPS];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        jr[r] = u0 + r < nu ? static_cast<int>(sb[(u0 + r) * 64]) : 0;
+        const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
+#pragma unroll
+        for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
         double part = 0.0;
 #pragma unroll
-        for (int c = 0; c < KSTEPS; ++c) {
-          const V kv = load_vec16<V>(krow + 16 * c);
+        for (int c = 0; c < KSTEPS; ++c)
 #pragma unroll
           for (int i = 0; i < 8; ++i)
             part += static_cast<double>(static_cast<float>(bq[c][i])) *
-                    static_cast<double>(static_cast<float>(kv[i]));
-        }
+                    static_cast<double>(static_cast<float>(kv[r][c][i]));
         part += __shfl_xor(part, 32);
-        sc = Elem<T>::round(static_cast<float>(part));
+        const float sc = Elem<T>::round(static_cast<float>(part));
+        if (u0 + r < nu && sc > -INFINITY) insert_exact<M>(fv, fi, sc, jr[r]);
       }
-      if (sc > -INFINITY) insert_exact<M>(fv, fi, sc, j);
     }
   }
   if (!live || half != 0) return;
