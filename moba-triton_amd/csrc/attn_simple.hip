@@ -22,6 +22,8 @@
 // touches is staged in LDS as float32 so each product is formed once.
 #include "attn_common.h"
 
+#include <type_traits>
+
 namespace moba {
 
 constexpr int kE = 16;    // entries per group, forward / dq kernels
@@ -388,22 +390,30 @@ combine_kernel(const float* __restrict__ part_m, const float* __restrict__ part_
   if (lse && d0 == 0) lse[row] = m_g + log2f(ls);
 }
 
-template <typename T>
+// delta[row] = sum_d O[row, d] * dO[row, d]. L lanes own one token-major
+// row (8 features each, one vector load per tensor), so a wave streams
+// 64 / L whole rows per instruction; the L partial sums meet by shuffles.
+template <typename T, int L>
 __global__ void __launch_bounds__(256)
 delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, float* __restrict__ delta,
-             int64_t n_rows, int64_t S, int64_t h_q, int64_t D) {
-  // One wave per query row; lanes stride the features.
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
-  const int lane = threadIdx.x & 63;
-  if (row >= n_rows) return;
-  const int64_t bh = row / S, t = row % S;
-  const int64_t b = bh / h_q, h = bh % h_q;
-  const int64_t base = ((b * S + t) * h_q + h) * D;
+             int64_t n_rows, int64_t S, int64_t h_q) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gid / L;  // token-major: (b * S + t) * h_q + h
+  const int sub = static_cast<int>(gid % L);
   float acc = 0.f;
-  for (int64_t d = lane; d < D; d += 64)
-    acc = fmaf(Elem<T>::load(o, base + d), Elem<T>::load(dout, base + d), acc);
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-  if (lane == 0) delta[row] = acc;
+  if (row < n_rows) {
+    float x[8], y[8];
+    load8<T>(o + row * (8 * L) + 8 * sub, x);
+    load8<T>(dout + row * (8 * L) + 8 * sub, y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = fmaf(x[i], y[i], acc);
+  }
+#pragma unroll
+  for (int w = L / 2; w > 0; w >>= 1) acc += __shfl_xor(acc, w);
+  if (row < n_rows && sub == 0) {
+    const int64_t h = row % h_q, bt = row / h_q;
+    delta[(bt / S * h_q + h) * S + bt % S] = acc;
+  }
 }
 
 // One lane per (query, 8 features); a slot counts only if the forward wrote
@@ -572,11 +582,26 @@ extern "C" int moba_bwd_delta(const void* out, const void* dout, float* delta, i
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
   if (!out || !dout || !delta) return fail(MOBA_ERR_INVALID, "null pointer");
   const int64_t n_rows = batch * h_q * seq_len;
-  dim3 grid(static_cast<unsigned>(cdiv(n_rows * 64, 256)));
+  const int64_t lanes = head_dim / 8;
+  if (head_dim % 8 != 0 || lanes > 64 || (lanes & (lanes - 1)) != 0)
+    return fail(MOBA_ERR_UNSUPPORTED, "delta: head_dim must be 8 times a power of two <= 512");
+  dim3 grid(static_cast<unsigned>(cdiv(n_rows * lanes, 256)));
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
-    hipLaunchKernelGGL(delta_kernel<T>, grid, dim3(256), 0, as_stream(stream),
-                       static_cast<const T*>(out), static_cast<const T*>(dout), delta, n_rows,
-                       seq_len, h_q, head_dim);
+    auto go = [&](auto lanes_c) {
+      constexpr int Lc = decltype(lanes_c)::value;
+      hipLaunchKernelGGL((delta_kernel<T, Lc>), grid, dim3(256), 0, as_stream(stream),
+                         static_cast<const T*>(out), static_cast<const T*>(dout), delta,
+                         n_rows, seq_len, h_q);
+    };
+    switch (lanes) {
+      case 1: go(std::integral_constant<int, 1>{}); break;
+      case 2: go(std::integral_constant<int, 2>{}); break;
+      case 4: go(std::integral_constant<int, 4>{}); break;
+      case 8: go(std::integral_constant<int, 8>{}); break;
+      case 16: go(std::integral_constant<int, 16>{}); break;
+      case 32: go(std::integral_constant<int, 32>{}); break;
+      default: go(std::integral_constant<int, 64>{}); break;
+    }
     return check_launch("moba_bwd_delta");
   });
 }

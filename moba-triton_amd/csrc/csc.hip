@@ -153,30 +153,36 @@ scan_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ col_offse
   if (threadIdx.x == 0) off[n_blocks] = carry;
 }
 
-// order[rank(c)] = c with rank by (count desc, id asc).
+// order[rh, rank] = column with that rank under (nnz desc, column asc).
+// Eight lanes share one column and split its comparisons; their partial
+// ranks meet by shuffles.
 __global__ void __launch_bounds__(256)
 order_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ order,
              int64_t n_blocks) {
   __shared__ int32_t tile[4096];
   const int64_t rh = blockIdx.y;
   const int32_t* cnt = col_nnz + rh * n_blocks;
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int sub = threadIdx.x & 7;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 8) + (threadIdx.x >> 3);
   const int32_t mine = c < n_blocks ? cnt[c] : 0;
-  int64_t rank = 0;
+  int rank = 0;
   for (int64_t base = 0; base < n_blocks; base += 4096) {
     const int64_t len = n_blocks - base < 4096 ? n_blocks - base : 4096;
     __syncthreads();
     for (int64_t i = threadIdx.x; i < len; i += blockDim.x) tile[i] = cnt[base + i];
     __syncthreads();
     if (c < n_blocks) {
-      for (int64_t i = 0; i < len; ++i) {
+      for (int64_t i = sub; i < len; i += 8) {
         const int32_t o = tile[i];
         const int64_t id = base + i;
         rank += (o > mine || (o == mine && id < c)) ? 1 : 0;
       }
     }
   }
-  if (c < n_blocks) order[rh * n_blocks + rank] = static_cast<int32_t>(c);
+  rank += __shfl_xor(rank, 1);
+  rank += __shfl_xor(rank, 2);
+  rank += __shfl_xor(rank, 4);
+  if (c < n_blocks && sub == 0) order[rh * n_blocks + rank] = static_cast<int32_t>(c);
 }
 
 }  // namespace moba
@@ -237,7 +243,7 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024), 0, s,
                      col_nnz, col_offsets, n_blocks);
   hipLaunchKernelGGL(order_kernel,
-                     dim3(static_cast<unsigned>(cdiv(n_blocks, 256)),
+                     dim3(static_cast<unsigned>(cdiv(n_blocks, 32)),
                           static_cast<unsigned>(batch * h_kv)),
                      dim3(256), 0, s, col_nnz, order, n_blocks);
   if (tiled)
