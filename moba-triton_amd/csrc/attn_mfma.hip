@@ -22,6 +22,8 @@
 // query's fixed slot.
 #include "attn_common.h"
 
+#include <type_traits>
+
 namespace moba {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -195,27 +197,45 @@ attend_mfma_kernel(AttnArgs a) {
     const int64_t rrel = static_cast<int64_t>(row) - c.key0;
     const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
     const int lim = live ? min(key_lim - 1, row_lim) : -1;  // last visible key
-    float m = -INFINITY;
+    float m = -INFINITY, l = 0.f;
+    if (__all(!live || lim == BS - 1)) {
+      // Every key of the block is visible to every live query of the group
+      // (a full, strictly past block): no masks; the scale folds into one
+      // fma before the exp2 (scale > 0, so the max commutes with it).
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        const float x = key <= lim ? s[kt][v] * a.scale_log2 : -INFINITY;
-        s[kt][v] = x;
-        m = fmaxf(m, x);
+        for (int v = 0; v < 16; ++v) m = fmaxf(m, s[kt][v]);
+      m = fmaxf(m, __shfl_xor(m, 32)) * a.scale_log2;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[kt][v], a.scale_log2, -m));
+          s[kt][v] = p;
+          l += p;
+        }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          const float x = key <= lim ? s[kt][v] * a.scale_log2 : -INFINITY;
+          s[kt][v] = x;
+          m = fmaxf(m, x);
+        }
       }
-    }
-    m = fmaxf(m, __shfl_xor(m, 32));
-    float l = 0.f;
+      m = fmaxf(m, __shfl_xor(m, 32));
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        const float p = key <= lim ? __builtin_amdgcn_exp2f(s[kt][v] - m) : 0.f;
-        s[kt][v] = p;
-        l += p;
+        for (int v = 0; v < 16; ++v) {
+          const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          const float p = key <= lim ? __builtin_amdgcn_exp2f(s[kt][v] - m) : 0.f;
+          s[kt][v] = p;
+          l += p;
+        }
       }
     }
     l += __shfl_xor(l, 32);
