@@ -427,10 +427,11 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   constexpr int KSTEPS = D / 16;
   constexpr int KROW = D + 8;                      // staged kbar row stride (elements)
   constexpr int NT = WAVES * 64;
-  constexpr int KCH = (32 * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per stage
+  constexpr int SR = 64;                           // kbar rows per LDS stage (two chunks)
+  constexpr int KCH = (SR * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per stage
   constexpr float kTr = 0.0078125f * 1.01f;        // key truncation, relative
   __shared__ uint32_t s_buf[WAVES][CAP][64];
-  __shared__ __attribute__((aligned(16))) uint16_t s_kb[2][32 * KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t s_kb[2][SR * KROW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -493,18 +494,19 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   auto band = [&](float x) { return band_at(band_mag(x)); };
 
   const int n_chunks = (take > 0 && hz > 0) ? (hz + 31) / 32 : 0;
-  // kbar chunks of 32 rows are staged in LDS by the whole workgroup. Rows
-  // past the horizon are clamped to a valid row; their scores are masked
-  // (every such block is >= own for every query here).
-  // Chunk ch's rows wait in register slot ch % 3 (loaded three chunks ahead)
-  // until they are stored to LDS buffer ch % 2.
-  u32x4 kr0[KCH], kr1[KCH], kr2[KCH];
-  auto kload = [&](u32x4 (&r)[KCH], int ch) {
+  const int n_stages = (n_chunks + 1) / 2;
+  // kbar rows are staged in LDS by the whole workgroup, 64 rows (two chunks
+  // of 32) per stage. Rows past the horizon are clamped to a valid row;
+  // their scores are masked (every such block is >= own for every query
+  // here). Stage st waits in register slot st % 2 (loaded two stages ahead)
+  // until it is stored to LDS buffer st % 2.
+  u32x4 kr0[KCH], kr1[KCH];
+  auto kload = [&](u32x4 (&r)[KCH], int st) {
 #pragma unroll
     for (int u = 0; u < KCH; ++u) {
       const int i = tid + u * NT;
-      if (i < 32 * D / 8) {
-        const int blk = min(ch * 32 + i / (D / 8), hz - 1);
+      if (i < SR * D / 8) {
+        const int blk = min(st * SR + i / (D / 8), hz - 1);
         r[u] = *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(blk) * D +
                                               (i % (D / 8)) * 8);
       }
@@ -514,16 +516,9 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
     for (int u = 0; u < KCH; ++u) {
       const int i = tid + u * NT;
-      if (i < 32 * D / 8)
+      if (i < SR * D / 8)
         *reinterpret_cast<u32x4*>(&s_kb[buf][(i / (D / 8)) * KROW + (i % (D / 8)) * 8]) = r[u];
     }
-  };
-  auto score_chunk = [&](int buf) {
-    const uint16_t* arow = &s_kb[buf][col * KROW + 8 * half];
-    floatx16_t acc = {};
-#pragma unroll
-    for (int c = 0; c < KSTEPS; ++c) acc = Ops::mfma(load_vec16<V>(arow + 16 * c), bq[c], acc);
-    return acc;  // acc[v] scores block 32 ch + 8(v/4) + 4 half + v%4
   };
 
   // --- Pass 1: a lower bound on L from every chunk's maximum. ------------
@@ -538,24 +533,33 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   const int own_min = __builtin_amdgcn_readfirstlane(own);
   float theta = -INFINITY;
   auto stream_chunks = [&](auto&& body) {
-    // step(c): score chunk c, move chunk c + 1 from `next` into LDS, and
-    // request chunk c + 3 into the slot chunk c came from (`freed`).
-    auto step = [&](int c, const u32x4 (&next)[KCH], u32x4 (&freed)[KCH]) {
-      if (c >= n_chunks) return;
-      body(c, score_chunk(c & 1), c * 32 + 32 <= own_min);
-      if (c + 1 < n_chunks) kstore(next, (c + 1) & 1);
-      if (c + 3 < n_chunks) kload(freed, c + 3);
+    // step(st): score both chunks of stage st (two independent MFMA chains
+    // over one A-operand buffer), move stage st + 1 from `next` into LDS,
+    // and request stage st + 2 into the slot stage st came from (`freed`).
+    auto step = [&](int st, const u32x4 (&next)[KCH], u32x4 (&freed)[KCH]) {
+      if (st >= n_stages) return;
+      const uint16_t* arow = &s_kb[st & 1][col * KROW + 8 * half];
+      floatx16_t a0 = {}, a1 = {};
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) {
+        a0 = Ops::mfma(load_vec16<V>(arow + 16 * c), bq[c], a0);
+        a1 = Ops::mfma(load_vec16<V>(arow + 32 * KROW + 16 * c), bq[c], a1);
+      }
+      // a?[v] scores block 32 ch + 8(v/4) + 4 half + v%4
+      const int c0 = 2 * st;
+      body(c0, a0, c0 * 32 + 32 <= own_min);
+      if (c0 + 1 < n_chunks) body(c0 + 1, a1, c0 * 32 + 64 <= own_min);
+      if (st + 1 < n_stages) kstore(next, (st + 1) & 1);
+      if (st + 2 < n_stages) kload(freed, st + 2);
       __syncthreads();
     };
     kload(kr0, 0);
-    if (n_chunks > 1) kload(kr1, 1);
-    if (n_chunks > 2) kload(kr2, 2);
+    if (n_stages > 1) kload(kr1, 1);
     kstore(kr0, 0);
     __syncthreads();
-    for (int ch = 0; ch < n_chunks; ch += 3) {
-      step(ch, kr1, kr0);
-      step(ch + 1, kr2, kr1);
-      step(ch + 2, kr0, kr2);
+    for (int st = 0; st < n_stages; st += 2) {
+      step(st, kr1, kr0);
+      step(st + 1, kr0, kr1);
     }
   };
   if (n_chunks > 0) {
@@ -789,7 +793,9 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
                        const Geometry& g, int take, int cur, const GateWs& ws,
                        hipStream_t st) {
   constexpr int WAVES = 4;
-  constexpr int CAP = M + 24;
+  // Per-lane key buffer: one chunk's 16 scores beyond the fold trigger, and
+  // room for the two lists during the final walk.
+  constexpr int CAP = 2 * M > M + 12 ? 2 * M : M + 12;
   // Sample list per lane: the take-th best of the union of both lanes'
   // lists (2K >= take) is the take-th best of some subset of the sample.
   constexpr int K = M <= 12 ? 5 : 9;
