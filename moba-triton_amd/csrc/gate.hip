@@ -6,29 +6,43 @@
 // padding as src/moba/kernels/gating.py:300-335 does. The score is the exact
 // dot product rounded once to float32 and once to the input dtype.
 //
-// Two kernels:
+// Kernels:
 //
-// * gate_mfma_kernel (bf16 / fp16, the product path). Each wave owns 32
-//   queries of one (row, query head). Block representatives stream past in
-//   chunks of 32; v_mfma_f32_32x32x16 computes an approximate float32 score
-//   tile S^T[block][query] with the query on the lane axis, so every lane
-//   holds 16 scores of one query and the top-k bookkeeping never crosses
-//   lanes. Scores above the lane's running threshold are appended to a
-//   per-lane LDS buffer; when a buffer fills, it is folded into a sorted
-//   register list of the M best approximate scores and the threshold rises
-//   to the M-th best. At the end the two lanes sharing a query merge their
-//   lists, and only candidates within the provable error band of the T-th
-//   best are rescored exactly (float64, sequential, same as the oracle).
-//   The error band: any float32 summation of D bf16 products is within
-//   D * 2^-24 * sum|q_d kbar_d| <= D * 2^-24 * |q| |kbar| of the exact dot;
-//   the kernel uses 2^-14 |q| max|kbar| (>= 16x that bound at D <= 128) and
-//   a 2^-6 relative gap so two values separated by more than the band can
-//   never round to the same bf16/fp16 score. A query whose evidence is
-//   insufficient (near-ties beyond the list capacity, e.g. constructed
-//   ties) is queued for the exact kernel; it is never guessed.
+// * gate_mfma_kernel (bf16 / fp16, the product path). A workgroup of four
+//   waves owns 128 consecutive queries of one (row, query head); a wave owns
+//   32, two lanes per query, each holding half of the query's features as
+//   the MFMA B operand. Block representatives (kbar) stream through LDS in
+//   stages of 64 rows; v_mfma_f32_32x32x16 scores a 32-block x 32-query
+//   tile per wave with the query on the lane axis, so each lane holds 16
+//   approximate float32 scores of its query per 32-block chunk and the
+//   bookkeeping never crosses lanes.
+//   - Pass 1 keeps, per lane, the K largest chunk maxima. The take-th
+//     largest of the pair's union is the take-th best of a subset of the
+//     query's candidates, hence a lower bound on L (the take-th best of
+//     all); theta = that bound - band.
+//   - Pass 2 appends every score above the lane's threshold (>= theta) with
+//     its block id to a per-lane LDS buffer, folding it into a sorted list
+//     of the M best when it may overflow (the threshold then rises to the
+//     M-th).
+//   - Decide: the pair merges its lists (k-th of union: L = take-th,
+//     N = (take + 1)-th, rej = the larger M-th). |approx - exact| <= E with
+//     E = 2^-14 |q| max|kbar| plus the denormal terms (any float32 sum of D
+//     <= 128 products is within D 2^-24 |q| |kbar|); band = 2E + a 2^-7
+//     relative gap, so two scores further apart than the band round to
+//     distinct bf16/fp16 values in the same order. The query is decidable
+//     when L - rej and L - theta exceed the band and nothing overflows.
+//     Entries that surely outrank N are selected outright; the others
+//     within the band of L are rescored exactly (float64 partial dots of the
+//     two lanes, rounded like the oracle) and ranked by (score desc, id asc).
+//   A query that is not decidable (near-ties beyond the lists, constructed
+//   ties, inf / NaN input) is queued; it is never guessed.
 //
-// * gate_exact_kernel (fp32, and the queue above). One thread per query,
-//   exact float64 scores for every candidate, streaming top-T in registers.
+// * gate_queue_kernel: one workgroup per queued query, exact scores for
+//   every candidate, lists merged across the workgroup.
+//
+// * gate_exact_kernel (fp32, take > 16 or unsupported shapes). One thread
+//   per query, exact float64 scores for every candidate, streaming top-T in
+//   registers.
 #include "common.h"
 
 namespace moba {
@@ -139,6 +153,22 @@ __device__ inline void insert_exact(float (&val)[M], int (&idx)[M], float s, int
       s = tv; j = ti;
       carry = true;
     }
+  }
+}
+
+// Branch-free insertion into a list sorted by value only (approximate scores;
+// ties among them are settled later by the exact rescoring).
+template <int M>
+__device__ inline void insert_approx(float (&val)[M], int (&idx)[M], float s, int j) {
+#pragma unroll
+  for (int p = 0; p < M; ++p) {
+    const bool gt = s > val[p];
+    const float nv = gt ? s : val[p];
+    const int ni = gt ? j : idx[p];
+    s = gt ? val[p] : s;
+    j = gt ? idx[p] : j;
+    val[p] = nv;
+    idx[p] = ni;
   }
 }
 
@@ -362,58 +392,14 @@ __device__ inline V load_vec16(const void* p) {
   return __builtin_bit_cast(V, u);
 }
 
-// Approximate-score keys. A key is the float32 approximate score with its
-// low 16 mantissa bits replaced by the block id, read through the
-// order-preserving map float bits <-> signed int (an involution), so that
-// integer max / min / med3 order keys by score, and the id rides along.
-// |value(key) - score| < 2^-7 |value(key)| (1 + 2^-7) for normal scores, and
-// below 2^-133 in the subnormal range.
-__device__ inline int ord_map(uint32_t bits) {
-  return static_cast<int>(bits ^ (static_cast<uint32_t>(static_cast<int>(bits) >> 31) >> 1));
-}
-__device__ inline float key_value(int k) { return u2f(static_cast<uint32_t>(ord_map(static_cast<uint32_t>(k)))); }
-__device__ inline int key_id(int k) { return ord_map(static_cast<uint32_t>(k)) & 0xffff; }
-constexpr int kNoKey = -2147483647 - 1;  // below every key (no entry)
-
-__device__ inline int med3i(int a, int b, int c) {
-  int d;
-  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
-// Inserts x into a list sorted descending; the smallest entry falls off.
+// Inserts x into a list of values sorted descending; the smallest falls off.
 // New entry p is the median of old entries p - 1, p and x.
-template <int M>
-__device__ inline void insert_key(int (&l)[M], int x) {
-#pragma unroll
-  for (int p = M - 1; p > 0; --p) l[p] = med3i(l[p - 1], l[p], x);
-  l[0] = max(l[0], x);
-}
-// Same for floats (values only).
 template <int K>
 __device__ inline void insert_value(float (&l)[K], float x) {
 #pragma unroll
   for (int p = K - 1; p > 0; --p) l[p] = __builtin_amdgcn_fmed3f(l[p - 1], l[p], x);
   l[0] = fmaxf(l[0], x);
 }
-// k-th largest key (1-based, k <= M) of the union of two descending lists
-// of distinct keys; kNoKey when the union holds fewer than k keys.
-template <int M>
-__device__ inline int kth_key(const int (&A)[M], const int (&B)[M], int k) {
-  int best = kNoKey;
-#pragma unroll
-  for (int i = 0; i <= M; ++i) {
-    if (i > k) break;
-    const int a = i == 0 ? 0x7fffffff : A[i - 1];
-    const int jb = k - i;
-    int b = 0x7fffffff;
-#pragma unroll
-    for (int u = 0; u < M; ++u) b = (u == jb - 1) ? B[u] : b;
-    if (jb > M) b = kNoKey;
-    best = max(best, min(a, b));
-  }
-  return best;
-}
-
 template <typename T, int D, int M, int K, int CAP, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64, (D == 64 && M <= 12) ? 3 : 1)
 gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
@@ -429,8 +415,8 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   constexpr int NT = WAVES * 64;
   constexpr int SR = 64;                           // kbar rows per LDS stage (two chunks)
   constexpr int KCH = (SR * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per stage
-  constexpr float kTr = 0.0078125f * 1.01f;        // key truncation, relative
-  __shared__ uint32_t s_buf[WAVES][CAP][64];
+  __shared__ float s_val[WAVES][CAP][64];
+  __shared__ uint16_t s_id[WAVES][CAP][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_kb[2][SR * KROW];
 
   const int tid = threadIdx.x;
@@ -488,9 +474,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // the storage dtype, in key order. band_mag also covers the magnitude of
   // x - band(x) itself.
   auto band_mag = [&](float x) { return (fabsf(x) + 2.f * E) * 1.05f + 2.f * Ops::kGapAbs; };
-  auto band_at = [&](float m) {
-    return 2.f * E + 2.f * kTr * m + Ops::kGapRel * (m + E) + Ops::kGapAbs;
-  };
+  auto band_at = [&](float m) { return 2.f * E + Ops::kGapRel * (m + E) + Ops::kGapAbs; };
   auto band = [&](float x) { return band_at(band_mag(x)); };
 
   const int n_chunks = (take > 0 && hz > 0) ? (hz + 31) / 32 : 0;
@@ -584,29 +568,30 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
     for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
     const float tau = kth_of_union<K>(tk, pk, take);
-    // The cut below is L's key minus band(L); the key may sit up to
-    // kTr |L| under the score, so theta carries that much more slack.
-    if (tau > -INFINITY) theta = tau - band(tau) - 2.f * kTr * band_mag(tau);
+    if (tau > -INFINITY) theta = tau - band(tau);
   }
   // Collection threshold: a > thr0 is a >= theta.
   const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
   // --- Pass 2: every chunk again. Each score above the lane's threshold
-  // (rare: theta sits within the decision band of L) becomes a key in the
-  // lane's LDS buffer; a buffer that may overflow on the next chunk is
-  // folded into the lane's sorted list of its M best keys, and the
-  // threshold rises to the M-th.
-  int lk[M];
+  // (rare: theta sits within the decision band of L) is appended, with its
+  // block id, to the lane's LDS buffer; a buffer that may overflow on the
+  // next chunk is folded into the lane's list of its M best scores (value
+  // order; ties are settled by the exact rescoring), and the threshold
+  // rises to the M-th.
+  float lv[M];
+  int li[M];
 #pragma unroll
-  for (int p = 0; p < M; ++p) lk[p] = kNoKey;
-  uint32_t* sb = &s_buf[wave][0][lane];  // this lane's column of the buffer
+  for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
+  float* sv = &s_val[wave][0][lane];     // this lane's column of the buffers
+  uint16_t* si = &s_id[wave][0][lane];
   if (n_chunks > 0) {
     float thr = thr0;
     int cnt = 0;
     auto fold = [&]() {
-      for (int e = 0; e < cnt; ++e) insert_key<M>(lk, ord_map(sb[e * 64]));
+      for (int e = 0; e < cnt; ++e) insert_approx<M>(lv, li, sv[e * 64], si[e * 64]);
       cnt = 0;
-      if (lk[M - 1] != kNoKey) thr = fmaxf(thr0, key_value(lk[M - 1]));
+      if (lv[M - 1] > -INFINITY) thr = fmaxf(thr0, lv[M - 1]);
     };
     // A score is appended only when it beats the threshold; the wave-wide
     // ballot skips the append for the (common) scores no lane keeps.
@@ -614,7 +599,8 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       const bool hit = a > thr;
       if (__ballot(hit) != 0) {
         if (hit) {
-          sb[cnt * 64] = (f2u(a) & 0xffff0000u) | id;
+          sv[cnt * 64] = a;
+          si[cnt * 64] = static_cast<uint16_t>(id);
           ++cnt;
         }
       }
@@ -637,84 +623,84 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   }
   int n_in_list = 0;
 #pragma unroll
-  for (int p = 0; p < M; ++p) n_in_list += lk[p] != kNoKey ? 1 : 0;
+  for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
 
   // --- Merge the two half-lists of this query and decide. -----------------
-  // Every key k carries |value(k) - exact| <= E + kTr |value(k)|. Scores
-  // >= theta left out of a lane's list are <= its M-th key (rej; none while
-  // the list is not full); scores below theta never entered.
-  const int rej_mine = (n_in_list == M) ? lk[M - 1] : kNoKey;
-  const int rejk = max(rej_mine, __shfl_xor(rej_mine, 32));
-  int pk[M];
+  // Every approximate score a carries |a - exact| <= E. Scores >= theta left
+  // out of a lane's list are <= its M-th (rej; none while the list is not
+  // full); scores below theta never entered.
+  const float rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
+  const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
+  float pv[M];
+  int pi[M];
 #pragma unroll
-  for (int p = 0; p < M; ++p) pk[p] = __shfl_xor(lk[p], 32);
-  // L: the take-th key of the union; N: the (take + 1)-th.
-  const int Lk = take > 0 ? kth_key<M>(lk, pk, take) : kNoKey;
-  const int Nk = take > 0 ? kth_key<M>(lk, pk, take + 1) : kNoKey;
-  const float Lf = Lk != kNoKey ? key_value(Lk) : -INFINITY;
-  const float Nf = Nk != kNoKey ? key_value(Nk) : -INFINITY;
-  const float rejf = rejk != kNoKey ? key_value(rejk) : -INFINITY;
+  for (int p = 0; p < M; ++p) {
+    pv[p] = __shfl_xor(lv[p], 32);
+    pi[p] = __shfl_xor(li[p], 32);
+  }
+  // L: the take-th approximate score of the union; N: the (take + 1)-th.
+  const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
+  const float N = take > 0 ? kth_of_union<M>(lv, pv, take + 1) : -INFINITY;
   bool ok = true;
   float cut = -INFINITY;
-  if (take > 0 && Lf > -INFINITY) {
-    const float mag = band_mag(Lf);
+  if (take > 0 && L > -INFINITY) {
+    const float mag = band_mag(L);
     if (!(mag < Ops::kMaxFinite)) ok = false;
-    if (rejf > -INFINITY &&
-        !(Lf - rejf > band_at(fmaxf(mag, band_mag(rejf))))) ok = false;
-    cut = Lf - band_at(mag);
+    if (rej > -INFINITY && !(L - rej > band_at(fmaxf(mag, band_mag(rej))))) ok = false;
+    cut = L - band_at(mag);
     if (!(cut >= theta)) ok = false;  // a needed candidate may lie below theta
   }
   // q or kbar carries inf / NaN, or a float32 score could overflow.
   if (take > 0 && !(qnorm * knorm < 3.0e38f)) ok = false;
-  // Union entries >= cut: those that surely outrank the (take + 1)-th key
+
+  // Union entries >= cut: those that surely outrank the (take + 1)-th score
   // (and so everything from there down) are selected outright; the rest
   // are rescored exactly (float64) by the two lanes together, each forming
-  // the partial dot over the features it holds. Both lanes walk the union
-  // in the same order (half 0's list first) and keep identical lists, in
-  // which an outright selection ranks first (score +inf, then by id).
-  float fv[M];
-  int fi[M];
+  // the partial dot over the features it holds, and ranked by (score desc,
+  // id asc). Both lanes walk the union in the same order (half 0's list
+  // first) and reach identical results. Outright ids collect in a per-lane
+  // LDS list in the (now idle) kbar staging buffer, uncertain ids in the
+  // lane's candidate buffer.
+  constexpr int TS = M <= 12 ? 8 : 16;  // most past blocks one query selects
+  uint32_t* ss = reinterpret_cast<uint32_t*>(&s_kb[0][0]) + wave * TS * 64 + lane;
+  float fv[TS];
+  int fi[TS];
 #pragma unroll
-  for (int p = 0; p < M; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
+  for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
+  int ns = 0;
+  uint32_t* su = reinterpret_cast<uint32_t*>(sv);
   if (ok && take > 0 && live) {
-    const float hiN = Nk != kNoKey ? Nf + kTr * fabsf(Nf) + E : -INFINITY;
-    // The union in walk order, through the (now idle) buffer: 2M <= CAP.
-#pragma unroll
-    for (int p = 0; p < M; ++p) {
-      sb[p * 64] = static_cast<uint32_t>(half == 0 ? lk[p] : pk[p]);
-      sb[(M + p) * 64] = static_cast<uint32_t>(half == 0 ? pk[p] : lk[p]);
-    }
-    // Classify; uncertain ids go back into the buffer (slot u <= p, already
-    // read), then are rescored R at a time so their row loads overlap.
+    const float hiN = N > -INFINITY ? N + E : -INFINITY;
     int nu = 0;
-#pragma unroll 1
+#pragma unroll
     for (int p = 0; p < 2 * M; ++p) {
-      const int k = static_cast<int>(sb[p * 64]);
-      if (k == kNoKey) continue;
-      const float x = key_value(k);
-      if (!(x >= cut)) continue;
-      const int j = key_id(k);
-      bool sure = Nk == kNoKey;
+      const bool own_list = (p < M) == (half == 0);
+      const float x = own_list ? lv[p % M] : pv[p % M];
+      const int j = own_list ? li[p % M] : pi[p % M];
+      if (!(x > -INFINITY && x >= cut)) continue;
+      bool sure = !(N > -INFINITY);
       if (!sure) {
-        const float lo = x - kTr * fabsf(x) - E;
-        const float mi = fmaxf(fabsf(x) * (1.f + kTr) + E, fabsf(hiN));
+        const float lo = x - E;
+        const float mi = fmaxf(fabsf(x) + E, fabsf(hiN));
         sure = lo - hiN > Ops::kGapRel * mi + Ops::kGapAbs;
       }
       if (sure) {
-        insert_exact<M>(fv, fi, INFINITY, j);
+        ss[ns * 64] = static_cast<uint32_t>(j);
+        ++ns;
       } else {
-        sb[nu * 64] = static_cast<uint32_t>(j);
+        if (nu < CAP) su[nu * 64] = static_cast<uint32_t>(j);
         ++nu;
       }
     }
+    if (nu > CAP) ok = false;  // more near-ties than the buffer holds
     constexpr int R = 2;
 #pragma unroll 1
-    for (int u0 = 0; u0 < nu; u0 += R) {
+    for (int u0 = 0; ok && u0 < nu; u0 += R) {
       int jr[R];
       V kv[R][KSTEPS];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        jr[r] = u0 + r < nu ? static_cast<int>(sb[(u0 + r) * 64]) : 0;
+        jr[r] = u0 + r < nu ? static_cast<int>(su[(u0 + r) * 64]) : 0;
         const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
 #pragma unroll
         for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
@@ -730,7 +716,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                     static_cast<double>(static_cast<float>(kv[r][c][i]));
         part += __shfl_xor(part, 32);
         const float sc = Elem<T>::round(static_cast<float>(part));
-        if (u0 + r < nu && sc > -INFINITY) insert_exact<M>(fv, fi, sc, jr[r]);
+        if (u0 + r < nu && sc > -INFINITY) insert_exact<TS>(fv, fi, sc, jr[r]);
       }
     }
   }
@@ -741,11 +727,18 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     queue[slot] = (r * h_q + hq) * rows_per_seq + t;
     return;
   }
-  int n_sel = 0;
+  // Selected: the outright ids, then the best (take - ns) rescored ones.
+  int n_sel = ns;
 #pragma unroll
-  for (int p = 0; p < M; ++p)
-    if (p < take && fv[p] > -INFINITY) n_sel = p + 1;
-  emit_sorted<M>(fi, n_sel, own, cur != 0, out + qid * slots, slots);
+  for (int p = 0; p < TS; ++p)
+    if (p < take - ns && fv[p] > -INFINITY) {
+      ss[(ns + p) * 64] = static_cast<uint32_t>(fi[p]);
+      n_sel = ns + p + 1;
+    }
+  int sel[TS];
+#pragma unroll
+  for (int p = 0; p < TS; ++p) sel[p] = p < n_sel ? static_cast<int>(ss[p * 64]) : 0x7fffffff;
+  emit_sorted<TS>(sel, n_sel, own, cur != 0, out + qid * slots, slots);
 }
 
 // ---------------------------------------------------------------------------
@@ -793,9 +786,9 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
                        const Geometry& g, int take, int cur, const GateWs& ws,
                        hipStream_t st) {
   constexpr int WAVES = 4;
-  // Per-lane key buffer: one chunk's 16 scores beyond the fold trigger, and
-  // room for the two lists during the final walk.
-  constexpr int CAP = 2 * M > M + 12 ? 2 * M : M + 12;
+  // Per-lane candidate buffer: one chunk's 16 scores beyond the fold
+  // trigger (cnt > CAP - 16); also holds the uncertain ids of the decision.
+  constexpr int CAP = M + 8;
   // Sample list per lane: the take-th best of the union of both lanes'
   // lists (2K >= take) is the take-th best of some subset of the sample.
   constexpr int K = M <= 12 ? 5 : 9;
