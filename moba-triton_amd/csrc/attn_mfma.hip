@@ -216,27 +216,26 @@ attend_mfma_kernel(AttnArgs a) {
           l += p;
         }
     } else {
+      // Same arithmetic as above on the visible keys (so a query's result
+      // never depends on which queries share its group).
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          const float x = key <= lim ? s[kt][v] * a.scale_log2 : -INFINITY;
-          s[kt][v] = x;
-          m = fmaxf(m, x);
+          m = fmaxf(m, key <= lim ? s[kt][v] : -INFINITY);
         }
-      }
-      m = fmaxf(m, __shfl_xor(m, 32));
+      m = fmaxf(m, __shfl_xor(m, 32)) * a.scale_log2;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
+      for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          const float p = key <= lim ? __builtin_amdgcn_exp2f(s[kt][v] - m) : 0.f;
+          const float p =
+              key <= lim ? __builtin_amdgcn_exp2f(fmaf(s[kt][v], a.scale_log2, -m)) : 0.f;
           s[kt][v] = p;
           l += p;
         }
-      }
     }
     l += __shfl_xor(l, 32);
 

@@ -74,38 +74,40 @@ static GateWs gate_ws(void* base, int64_t rows, int64_t h_kv, int64_t queue_cap)
 }
 
 // ---------------------------------------------------------------------------
-// Prologue: max |kbar_j| per (row, kv head); clears the queue counter.
+// Prologue: max |kbar_j| per (row, kv head), as float bits (non-negative, so
+// unsigned order is value order and NaN, the largest pattern, survives).
+// gate_init_kernel clears the maxima and the queue counter; gate_prep_kernel
+// gives each block of kbar a thread and folds the maxima in with atomicMax.
 // ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+gate_init_kernel(unsigned* __restrict__ norm_bits, int64_t n, int* __restrict__ counter) {
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) norm_bits[i] = 0u;
+  if (threadIdx.x == 0) *counter = 0;
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256)
 gate_prep_kernel(const T* __restrict__ kbar, const int32_t* __restrict__ cu,
                  int64_t S, int64_t h_kv, int64_t n_blocks, int64_t D, int64_t bs,
-                 float* __restrict__ norm_out, int* __restrict__ counter) {
-  const int64_t rh = blockIdx.x;
-  if (rh == 0 && threadIdx.x == 0) *counter = 0;
+                 unsigned* __restrict__ norm_bits) {
+  const int64_t rh = blockIdx.y;
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   // Only the blocks a sequence owns hold data; the tail of a packed kbar row
-  // is never read by the gate and may be uninitialised.
+  // is never read by the gate.
   const SeqSpan sp = seq_span(cu, rh / h_kv, S);
   const int64_t owned = (sp.len + bs - 1) / bs < n_blocks ? (sp.len + bs - 1) / bs : n_blocks;
-  __shared__ float red[256];
-  float best = 0.f;
-  const T* base = kbar + rh * n_blocks * D;
-  for (int64_t j = threadIdx.x; j < owned; j += blockDim.x) {
+  unsigned best = 0u;
+  if (j < owned) {
+    const T* row = kbar + (rh * n_blocks + j) * D;
     float ss = 0.f;
     for (int64_t d = 0; d < D; ++d) {
-      float x = Elem<T>::load(base, j * D + d);
-      ss += x * x;
+      const float x = Elem<T>::load(row, d);
+      ss = fmaf(x, x, ss);
     }
-    best = fmaxf(best, sqrtf(ss));  // fmaxf drops NaN; inf propagates
+    best = f2u(sqrtf(ss)) & 0x7fffffffu;  // drop the sign of a NaN
   }
-  red[threadIdx.x] = best;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-    __syncthreads();
-  }
-  // Slack for the float sum of squares and sqrtf (a few ulp).
-  if (threadIdx.x == 0) norm_out[rh] = red[0] * 1.0001f + 1e-30f;
+  for (int off = 32; off > 0; off >>= 1) best = max(best, static_cast<unsigned>(__shfl_xor(static_cast<int>(best), off)));
+  if ((threadIdx.x & 63) == 0 && best != 0u) atomicMax(norm_bits + rh, best);
 }
 
 // ---------------------------------------------------------------------------
@@ -467,7 +469,8 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Accumulation error, plus what flushing denormal operands could drop:
   // each flushed factor is below kDenorm and its partner below |q| or |kbar|.
   const float qnorm = sqrtf(qn) * 1.0001f;
-  const float knorm = kbar_norm[r * h_kv + hk];
+  // Slack for the float sum of squares and sqrtf (a few ulp).
+  const float knorm = kbar_norm[r * h_kv + hk] * 1.0001f + 1e-30f;
   const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
   // Decision band around a key value x: two scores whose keys lie more than
   // band(x) apart (magnitudes <= band_mag(x)) round to distinct values of
@@ -819,10 +822,14 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
       ws_bytes < 256 + align256(sizeof(float) * g.rows * g.h_kv) + sizeof(int64_t) * qcap)
     return fail(MOBA_ERR_WORKSPACE, "gate workspace too small");
   GateWs ws = gate_ws(workspace, g.rows, g.h_kv, qcap);
-  hipLaunchKernelGGL(gate_prep_kernel<T>, dim3(static_cast<unsigned>(g.rows * g.h_kv)),
+  unsigned* norm_bits = reinterpret_cast<unsigned*>(ws.kbar_norm);
+  hipLaunchKernelGGL(gate_init_kernel, dim3(1), dim3(256), 0, st, norm_bits,
+                     g.rows * g.h_kv, ws.counter);
+  hipLaunchKernelGGL(gate_prep_kernel<T>,
+                     dim3(static_cast<unsigned>(cdiv(g.n_blocks, 256)),
+                          static_cast<unsigned>(g.rows * g.h_kv)),
                      dim3(256), 0, st, static_cast<const T*>(kbar), cu, g.seq_len,
-                     g.h_kv, g.n_blocks, g.head_dim, g.block_size, ws.kbar_norm,
-                     ws.counter);
+                     g.h_kv, g.n_blocks, g.head_dim, g.block_size, norm_bits);
   int rc = check_launch("moba_gate (prep)");
   if (rc) return rc;
   if (g.head_dim == 64) {
