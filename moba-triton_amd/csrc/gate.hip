@@ -526,11 +526,19 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     auto step = [&](int st, const u32x4 (&next)[KCH], u32x4 (&freed)[KCH]) {
       if (st >= n_stages) return;
       const uint16_t* arow = &s_kb[st & 1][col * KROW + 8 * half];
+      // All A operands of the stage are requested before the first MFMA.
+      V ka[2][KSTEPS];
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) {
+        ka[0][c] = load_vec16<V>(arow + 16 * c);
+        ka[1][c] = load_vec16<V>(arow + 32 * KROW + 16 * c);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
       floatx16_t a0 = {}, a1 = {};
 #pragma unroll
       for (int c = 0; c < KSTEPS; ++c) {
-        a0 = Ops::mfma(load_vec16<V>(arow + 16 * c), bq[c], a0);
-        a1 = Ops::mfma(load_vec16<V>(arow + 32 * KROW + 16 * c), bq[c], a1);
+        a0 = Ops::mfma(ka[0][c], bq[c], a0);
+        a1 = Ops::mfma(ka[1][c], bq[c], a1);
       }
       // a?[v] scores block 32 ch + 8(v/4) + 4 half + v%4
       const int c0 = 2 * st;
