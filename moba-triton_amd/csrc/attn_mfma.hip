@@ -182,13 +182,18 @@ attend_mfma_kernel(AttnArgs a) {
     csl = nsl;
     load_idx(g0 + 8 * 32, nr, nhd, nsl);
 
+    // S^T tiles: the KT chains interleave (independent MFMAs back to back),
+    // each K-step's operands read together.
     floatx16_t s[KT];
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      s[kt] = floatx16_t{};
-      const uint16_t* arow = &Ks[(kt * 32 + col) * KS + 8 * h];
+    for (int kt = 0; kt < KT; ++kt) s[kt] = floatx16_t{};
 #pragma unroll
-      for (int k = 0; k < D / 16; ++k) s[kt] = M::mma(ld16<V8>(arow + 16 * k), bq[k], s[kt]);
+    for (int k = 0; k < D / 16; ++k) {
+      V8 ka[KT];
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) ka[kt] = ld16<V8>(&Ks[(kt * 32 + col) * KS + 8 * h + 16 * k]);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) s[kt] = M::mma(ka[kt], bq[k], s[kt]);
     }
 
     // Masks, row max and sum. s[kt][v] is key 32kt + 8(v/4) + 4h + v%4.
