@@ -13,45 +13,59 @@
 
 namespace moba {
 
-// One thread per (row, kv head, block, 8-feature chunk): it walks the
-// block's tokens in order with one 16-byte load per token (the eight lanes
-// of a block read each key row whole), accumulating every feature exactly
-// in float64 in token order, then rounds once to float32 and to the dtype
-// and divides by the block's real occupancy.
-template <typename T>
+// TS threads per (row, kv head, block, 8-feature chunk). Each walks every
+// TS-th token of the block with one 16-byte load per token (eight lanes
+// read each key row whole) and accumulates the features in float64; the TS
+// partial sums then meet by shuffles. For 16-bit inputs (8- or 11-bit
+// significands, at most 128 terms) every partial and total float64 sum is
+// exact whenever the block's values span less than 2^38 in magnitude, so
+// the split changes nothing there; float32 inputs use TS = 1 (token order,
+// like the oracle). The total is rounded once to float32 and to the dtype,
+// then divided by the block's real occupancy.
+template <typename T, int TS>
 __global__ void __launch_bounds__(256)
 pool_kernel(const T* __restrict__ k, T* __restrict__ kbar,
             const int32_t* __restrict__ cu, int64_t S, int64_t h_kv,
             int64_t D, int64_t n_blocks, int64_t bs, int64_t n_items) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t cpr = D / 8;                 // 8-feature chunks per row
-  const int64_t item = gid / cpr;            // (r * h_kv + h) * n_blocks + blk
-  if (item >= n_items) return;
-  const int64_t d0 = (gid % cpr) * 8;
-  const int64_t blk = item % n_blocks;
-  const int64_t rh = item / n_blocks;
+  const int ts = static_cast<int>(gid % TS); // token phase (adjacent lanes)
+  const int64_t lin = gid / TS;
+  const int64_t item = lin / cpr;            // (r * h_kv + h) * n_blocks + blk
+  const bool ok = item < n_items;
+  const int64_t it = ok ? item : 0;
+  const int64_t d0 = (lin % cpr) * 8;
+  const int64_t blk = it % n_blocks;
+  const int64_t rh = it / n_blocks;
   const int64_t r = rh / h_kv, h = rh % h_kv;
   const SeqSpan sp = seq_span(cu, r, S);
-  T* dst = kbar + item * D + d0;
   const int64_t lo = blk * bs;
+  const int64_t hi = lo + bs < sp.len ? lo + bs : sp.len;
+  double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (ok && lo < sp.len) {
+    const T* src = k + ((sp.bos + lo + ts) * h_kv + h) * D + d0;
+    for (int64_t t = lo + ts; t < hi; t += TS, src += TS * h_kv * D) {
+      T x[8];
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<uint4*>(x) = *reinterpret_cast<const uint4*>(src);
+      } else {
+        reinterpret_cast<uint4*>(x)[0] = reinterpret_cast<const uint4*>(src)[0];
+        reinterpret_cast<uint4*>(x)[1] = reinterpret_cast<const uint4*>(src)[1];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += static_cast<double>(Elem<T>::load(x, i));
+    }
+  }
+#pragma unroll
+  for (int off = TS / 2; off > 0; off >>= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], off);
+  if (!ok || ts != 0) return;
+  T* dst = kbar + item * D + d0;
   if (lo >= sp.len) {  // a padded block slot of a short sequence: zeros
 #pragma unroll
     for (int i = 0; i < 8; ++i) Elem<T>::store(dst, i, 0.f);
     return;
-  }
-  const int64_t hi = lo + bs < sp.len ? lo + bs : sp.len;
-  double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const T* src = k + ((sp.bos + lo) * h_kv + h) * D + d0;
-  for (int64_t t = lo; t < hi; ++t, src += h_kv * D) {
-    T x[8];
-    if constexpr (sizeof(T) == 2) {
-      *reinterpret_cast<uint4*>(x) = *reinterpret_cast<const uint4*>(src);
-    } else {
-      reinterpret_cast<uint4*>(x)[0] = reinterpret_cast<const uint4*>(src)[0];
-      reinterpret_cast<uint4*>(x)[1] = reinterpret_cast<const uint4*>(src)[1];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += static_cast<double>(Elem<T>::load(x, i));
   }
   const float count = static_cast<float>(hi - lo);
 #pragma unroll
@@ -102,7 +116,9 @@ extern "C" int moba_pool(const void* k, void* kbar, const int32_t* cu_seqlens,
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
     if (head_dim % 8 == 0) {
       const int64_t n_items = g.rows * h_kv * n_blocks;
-      hipLaunchKernelGGL(pool_kernel<T>, dim3(static_cast<unsigned>(cdiv(n_items * (head_dim / 8), 256))),
+      constexpr int TS = sizeof(T) == 2 ? 4 : 1;
+      hipLaunchKernelGGL((pool_kernel<T, TS>),
+                         dim3(static_cast<unsigned>(cdiv(n_items * (head_dim / 8) * TS, 256))),
                          dim3(256), 0, as_stream(stream), static_cast<const T*>(k),
                          static_cast<T*>(kbar), cu_seqlens, seq_len, h_kv, head_dim, n_blocks,
                          block_size, n_items);
