@@ -122,13 +122,13 @@ def stage_times(s, dev, reps=5):
     st["combine"] = timed(lambda: combine_partials(*parts, q.dtype, return_lse=True),
                           reps, 1)[0]
     st["delta"] = timed(lambda: compute_delta(out, do), reps, 1)[0]
-    delta = compute_delta(out, do)
+    lse_delta = compute_delta(out, do, lse)
     dk, dv = torch.empty_like(k), torch.empty_like(v)
     dq_part = torch.empty((1, HEADS, s, TOPK, HEAD_DIM), device=dev, dtype=q.dtype)
 
     def bwd():
         _lib.call("moba_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(do),
-                  _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(index.col_nnz),
+                  _lib.ptr(lse_delta), _lib.ptr(index.col_nnz),
                   _lib.ptr(index.col_offsets), _lib.ptr(index.row_indices),
                   _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
                   _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),

@@ -47,7 +47,8 @@ enum moba_status {
 
 enum moba_dtype { MOBA_BF16 = 0, MOBA_FP16 = 1, MOBA_FP32 = 2 };
 
-/* Library identity. */
+/* Library identity. moba_abi_version() is 2: (m, l) and (lse, delta) travel
+ * as 8-byte pairs (version 1 took them as separate arrays). */
 int moba_abi_version(void);
 const char* moba_last_error(void);
 const char* moba_status_string(int status);
@@ -111,10 +112,11 @@ int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
 /*
  * KV-block-major attend: for every column, the keys of that block against
  * every query that selected it; writes per-slot un-normalised partials
- * part_m (row max of q.k * D^-1/2 * log2 e, log2 units), part_l (sum of
- * exp2), part_acc (sum of exp2 * v, in acc_dtype). Unwritten slots keep
- * part_m = -inf, which this call sets before the kernel runs.
- * part_m/part_l: [B, Hq, S, slots] fp32; part_acc [B, Hq, S, slots, D].
+ * m (row max of q.k * D^-1/2 * log2 e, log2 units), l (sum of exp2) and
+ * part_acc (sum of exp2 * v, in acc_dtype). m and l of a slot travel as
+ * one 8-byte pair: part_ml [B, Hq, S, slots, 2] fp32 = (m, l); part_acc
+ * [B, Hq, S, slots, D]. Unwritten slots keep m = -inf, which this call sets
+ * before the kernel runs.
  * Replaces attend_partials (src/moba/kernels/moba_fwd.py:566-665) and
  * moba_fwd_kernel (moba_fwd.py:230-425).
  */
@@ -122,7 +124,7 @@ int moba_attend(const void* q, const void* k, const void* v,
                 const int32_t* col_nnz, const int32_t* col_offsets,
                 const int32_t* row_indices, const int32_t* head_indices,
                 const int32_t* slot_of_pair, const int32_t* order,
-                float* part_m, float* part_l, void* part_acc,
+                float* part_ml, void* part_acc,
                 const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
                 int64_t max_seqlen, int64_t h_q, int64_t h_kv,
                 int64_t head_dim, int64_t n_blocks, int64_t block_size,
@@ -131,22 +133,26 @@ int moba_attend(const void* q, const void* k, const void* v,
 
 /*
  * LSE merge of the per-slot partials: out [B, S, Hq, D] (out_dtype) and,
- * when lse != NULL, lse [B, Hq, S] fp32 in log2 units. Slots with
- * part_m = -inf are skipped even if their l / acc hold NaN.
+ * when lse != NULL, lse [B, Hq, S] fp32 in log2 units. part_ml: the (m, l)
+ * pairs moba_attend writes. Slots with m = -inf are skipped even if their
+ * l / acc hold NaN.
  * Replaces combine_partials (src/moba/kernels/moba_fwd.py:668-725) and
  * moba_combine_kernel (moba_fwd.py:429-521).
  */
-int moba_combine(const float* part_m, const float* part_l,
+int moba_combine(const float* part_ml,
                  const void* part_acc, void* out, float* lse, int64_t batch,
                  int64_t seq_len, int64_t h_q, int64_t head_dim,
                  int64_t slots, int acc_dtype, int out_dtype, void* stream);
 
 /*
- * delta [B, Hq, S] fp32 = rowsum(dO * O). Replaces compute_delta
- * (src/moba/kernels/moba_bwd.py:454-470, kernel moba_bwd.py:135-160).
+ * delta = rowsum(dO * O) per (b, head, token). With lse == NULL, delta is
+ * [B, Hq, S] fp32; otherwise it receives the (lse, delta) pairs moba_bwd
+ * reads, [B, Hq, S, 2] fp32, lse copied from lse [B, Hq, S]. Replaces
+ * compute_delta (src/moba/kernels/moba_bwd.py:454-470, kernel
+ * moba_bwd.py:135-160).
  */
-int moba_bwd_delta(const void* out, const void* dout, float* delta,
-                   int64_t batch, int64_t seq_len, int64_t h_q,
+int moba_bwd_delta(const void* out, const void* dout, const float* lse,
+                   float* delta, int64_t batch, int64_t seq_len, int64_t h_q,
                    int64_t head_dim, int dtype, void* stream);
 
 /*
@@ -154,10 +160,11 @@ int moba_bwd_delta(const void* out, const void* dout, float* delta,
  * written, zero for unselected blocks) and one dQ partial per (query, slot):
  * dq_part [B, Hq, S, slots, D] (acc_dtype). Replaces the kernel launch in
  * moba_backward (src/moba/kernels/moba_bwd.py:506-579; kernel
- * moba_bwd.py:216-394). lse is log2 units as moba_combine writes it.
+ * moba_bwd.py:216-394). lse_delta: the (lse, delta) pairs moba_bwd_delta
+ * writes, lse in log2 units as moba_combine writes it.
  */
 int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
-             const float* lse, const float* delta, const int32_t* col_nnz,
+             const float* lse_delta, const int32_t* col_nnz,
              const int32_t* col_offsets, const int32_t* row_indices,
              const int32_t* head_indices, const int32_t* slot_of_pair,
              const int32_t* order, void* dk, void* dv, void* dq_part,
@@ -169,10 +176,12 @@ int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
 
 /*
  * dQ [B, S, Hq, D] = sum over written slots of dq_part, gated by the
- * forward's part_m written-marker. Replaces reduce_dq
- * (src/moba/kernels/moba_bwd.py:473-503, kernel moba_bwd.py:398-446).
+ * forward's m written-marker: slot j of row r reads part_m[(r * slots + j)
+ * * m_stride] (m_stride 2 for the pairs of moba_attend, 1 for a plain m
+ * array). Replaces reduce_dq (src/moba/kernels/moba_bwd.py:473-503, kernel
+ * moba_bwd.py:398-446).
  */
-int moba_dq_reduce(const void* dq_part, const float* part_m, void* dq,
+int moba_dq_reduce(const void* dq_part, const float* part_m, int64_t m_stride, void* dq,
                    int64_t batch, int64_t seq_len, int64_t h_q,
                    int64_t head_dim, int64_t slots, int acc_dtype,
                    int out_dtype, void* stream);

@@ -11,8 +11,7 @@ struct AttnArgs {
   const void* k;
   const void* v;
   const void* dout;       // backward only
-  const float* lse;       // backward only (log2 units)
-  const float* delta;     // backward only
+  const float* lse_delta; // backward only: (lse in log2 units, delta) per row
   const int32_t* col_nnz;
   const int32_t* col_offsets;
   const int32_t* row_indices;
@@ -20,8 +19,7 @@ struct AttnArgs {
   const int32_t* slot_of_pair;
   const int32_t* order;
   const int32_t* cu;
-  float* part_m;          // forward only
-  float* part_l;          // forward only
+  float* part_ml;         // forward only: (m, l) per (row, slot)
   void* part_acc;         // forward: acc partials; backward: dq partials
   void* dk;               // backward only
   void* dv;               // backward only

@@ -286,8 +286,7 @@ attend_mfma_kernel(AttnArgs a) {
       if (more) stage_q();
       noff = q_off(nr, nhd, nsl);  // waits for the index loads, before any store
       if (live && h == 0) {
-        a.part_m[dst] = m;
-        a.part_l[dst] = l;
+        *reinterpret_cast<float2*>(a.part_ml + 2 * dst) = make_float2(m, l);
       }
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
@@ -299,8 +298,7 @@ attend_mfma_kernel(AttnArgs a) {
       noff = q_off(nr, nhd, nsl);
       if (live) {
         if (h == 0) {
-          a.part_m[dst] = m;
-          a.part_l[dst] = l;
+          *reinterpret_cast<float2*>(a.part_ml + 2 * dst) = make_float2(m, l);
         }
         A* base = acc_out + dst * D + 4 * h;
 #pragma unroll
@@ -470,8 +468,9 @@ bwd_mfma_kernel(AttnArgs a) {
   bool pv[CH];  // chunk belongs to a live entry (zeroed when staged)
   float n_lse = 0.f, n_dl = 0.f;
   auto fetch = [&]() {  // step g + 1: rows via s_qoff, lse / delta via n_pr
-    n_lse = a.lse[n_pr];
-    n_dl = a.delta[n_pr];
+    const float2 ld = *reinterpret_cast<const float2*>(a.lse_delta + 2 * n_pr);
+    n_lse = ld.x;
+    n_dl = ld.y;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = tid + u * NT;

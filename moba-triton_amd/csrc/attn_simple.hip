@@ -103,8 +103,7 @@ attend_simple_kernel(AttnArgs a) {
       Ls[e] = l;
       if (Rs[e] >= 0) {
         const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
-        a.part_m[dst] = m;
-        a.part_l[dst] = l;
+        *reinterpret_cast<float2*>(a.part_ml + 2 * dst) = make_float2(m, l);
       }
     }
     __syncthreads();
@@ -169,8 +168,8 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
       const int32_t head = live ? a.head_indices[c.lo + e] : 0;
       Rs[threadIdx.x] = row;
       Hs[threadIdx.x] = head;
-      Lse[threadIdx.x] = live ? a.lse[part_row(a, c, row, head)] : 0.f;
-      Dl[threadIdx.x] = live ? a.delta[part_row(a, c, row, head)] : 0.f;
+      Lse[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head)] : 0.f;
+      Dl[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head) + 1] : 0.f;
     }
     __syncthreads();
     for (int64_t i = threadIdx.x; i < kBE * D; i += blockDim.x) {
@@ -260,8 +259,8 @@ bwd_dq_simple_kernel(AttnArgs a) {
       Rs[threadIdx.x] = row;
       Hs[threadIdx.x] = head;
       Zs[threadIdx.x] = live ? a.slot_of_pair[c.lo + e] : 0;
-      Lse[threadIdx.x] = live ? a.lse[part_row(a, c, row, head)] : 0.f;
-      Dl[threadIdx.x] = live ? a.delta[part_row(a, c, row, head)] : 0.f;
+      Lse[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head)] : 0.f;
+      Dl[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head) + 1] : 0.f;
     }
     __syncthreads();
     for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
@@ -357,25 +356,23 @@ __device__ inline void store8<float>(float* p, const float (&x)[8]) {
 // reference merge: the global max, then the rescaled sums.
 template <typename A, typename O>
 __global__ void __launch_bounds__(256)
-combine_kernel(const float* __restrict__ part_m, const float* __restrict__ part_l,
-               const A* __restrict__ part_acc, O* __restrict__ out, float* __restrict__ lse,
+combine_kernel(const float* __restrict__ part_ml, const A* __restrict__ part_acc, O* __restrict__ out, float* __restrict__ lse,
                int64_t n_rows, int64_t S, int64_t h_q, int64_t D, int64_t slots) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t per_row = D / 8;
   const int64_t row = gid / per_row;     // head-major (b * Hq + h) * S + t
   const int64_t d0 = (gid % per_row) * 8;
   if (row >= n_rows) return;
-  const float* m = part_m + row * slots;
-  const float* l = part_l + row * slots;
+  const float* ml = part_ml + row * slots * 2;  // (m, l) per slot
   float m_g = -INFINITY;
-  for (int64_t j = 0; j < slots; ++j) m_g = fmaxf(m_g, m[j]);
+  for (int64_t j = 0; j < slots; ++j) m_g = fmaxf(m_g, ml[2 * j]);
   float ls = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < slots; ++j) {
-    const float mi = m[j];
+    const float mi = ml[2 * j];
     if (mi > -INFINITY) {
       const float w = exp2f(mi - m_g);
-      ls += l[j] * w;
+      ls += ml[2 * j + 1] * w;
       float x[8];
       load8<A>(part_acc + (row * slots + j) * D + d0, x);
 #pragma unroll
@@ -395,8 +392,8 @@ combine_kernel(const float* __restrict__ part_m, const float* __restrict__ part_
 // 64 / L whole rows per instruction; the L partial sums meet by shuffles.
 template <typename T, int L>
 __global__ void __launch_bounds__(256)
-delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, float* __restrict__ delta,
-             int64_t n_rows, int64_t S, int64_t h_q) {
+delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, const float* __restrict__ lse,
+             float* __restrict__ delta, int64_t n_rows, int64_t S, int64_t h_q) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t row = gid / L;  // token-major: (b * S + t) * h_q + h
   const int sub = static_cast<int>(gid % L);
@@ -412,7 +409,9 @@ delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, float* __restr
   for (int w = L / 2; w > 0; w >>= 1) acc += __shfl_xor(acc, w);
   if (row < n_rows && sub == 0) {
     const int64_t h = row % h_q, bt = row / h_q;
-    delta[(bt / S * h_q + h) * S + bt % S] = acc;
+    const int64_t hm = (bt / S * h_q + h) * S + bt % S;
+    if (lse) *reinterpret_cast<float2*>(delta + 2 * hm) = make_float2(lse[hm], acc);
+    else delta[hm] = acc;
   }
 }
 
@@ -421,8 +420,8 @@ delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, float* __restr
 template <typename A, typename O>
 __global__ void __launch_bounds__(256)
 dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m,
-                 O* __restrict__ dq, int64_t n_rows, int64_t S, int64_t h_q, int64_t D,
-                 int64_t slots) {
+                 int64_t m_stride, O* __restrict__ dq, int64_t n_rows, int64_t S,
+                 int64_t h_q, int64_t D, int64_t slots) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t per_row = D / 8;
   const int64_t row = gid / per_row;
@@ -430,7 +429,7 @@ dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m
   if (row >= n_rows) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < slots; ++j)
-    if (part_m[row * slots + j] > -INFINITY) {
+    if (part_m[(row * slots + j) * m_stride] > -INFINITY) {
       float x[8];
       load8<A>(dq_part + (row * slots + j) * D + d0, x);
 #pragma unroll
@@ -513,7 +512,7 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
                            const int32_t* col_nnz, const int32_t* col_offsets,
                            const int32_t* row_indices, const int32_t* head_indices,
                            const int32_t* slot_of_pair, const int32_t* order,
-                           float* part_m, float* part_l, void* part_acc,
+                           float* part_ml, void* part_acc,
                            const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
                            int64_t max_seqlen, int64_t h_q, int64_t h_kv,
                            int64_t head_dim, int64_t n_blocks, int64_t block_size,
@@ -526,14 +525,15 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
                         slot_of_pair, order, cu_seqlens, batch, seq_len, max_seqlen, h_q,
                         h_kv, head_dim, n_blocks, block_size, slots, index_cap, causal);
   if (st) return st;
-  if (!part_m || !part_l || !part_acc) return fail(MOBA_ERR_INVALID, "null partials");
-  a.part_m = part_m; a.part_l = part_l; a.part_acc = part_acc;
+  if (!part_ml || !part_acc) return fail(MOBA_ERR_INVALID, "null partials");
+  a.part_ml = part_ml; a.part_acc = part_acc;
   hipStream_t s = as_stream(stream);
   // Unwritten slots must read as m = -inf: the marker combine and dq reduce
-  // rely on. Only part_m is cleared; l / acc of such slots are never read.
-  const int64_t n_m = (g.packed ? 1 : batch) * h_q * seq_len * slots;
+  // rely on. The (m, l) pairs are cleared whole; l / acc of such slots are
+  // never read.
+  const int64_t n_m = (g.packed ? 1 : batch) * h_q * seq_len * slots * 2;
   hipLaunchKernelGGL(fill_f32_kernel, dim3(static_cast<unsigned>(cdiv(n_m, 256) < 8192 ? cdiv(n_m, 256) : 8192)),
-                     dim3(256), 0, s, part_m, n_m, -INFINITY);
+                     dim3(256), 0, s, part_ml, n_m, -INFINITY);
   st = check_launch("moba_attend (fill)");
   if (st) return st;
   st = attend_mfma(a, dtype, acc_dtype, batch * h_kv, s);
@@ -553,30 +553,30 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
   });
 }
 
-extern "C" int moba_combine(const float* part_m, const float* part_l, const void* part_acc,
+extern "C" int moba_combine(const float* part_ml, const void* part_acc,
                             void* out, float* lse, int64_t batch, int64_t seq_len,
                             int64_t h_q, int64_t head_dim, int64_t slots, int acc_dtype,
                             int out_dtype, void* stream) {
   using namespace moba;
   if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0 || slots <= 0)
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
-  if (!part_m || !part_l || !part_acc || !out) return fail(MOBA_ERR_INVALID, "null pointer");
+  if (!part_ml || !part_acc || !out) return fail(MOBA_ERR_INVALID, "null pointer");
   if (head_dim % 8) return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
   const int64_t n_rows = batch * h_q * seq_len;
   dim3 grid(static_cast<unsigned>(cdiv(n_rows * (head_dim / 8), 256)));
   return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
     return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
       hipLaunchKernelGGL((combine_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
-                         part_m, part_l, static_cast<const A*>(part_acc), static_cast<O*>(out),
+                         part_ml, static_cast<const A*>(part_acc), static_cast<O*>(out),
                          lse, n_rows, seq_len, h_q, head_dim, slots);
       return check_launch("moba_combine");
     });
   });
 }
 
-extern "C" int moba_bwd_delta(const void* out, const void* dout, float* delta, int64_t batch,
-                              int64_t seq_len, int64_t h_q, int64_t head_dim, int dtype,
-                              void* stream) {
+extern "C" int moba_bwd_delta(const void* out, const void* dout, const float* lse,
+                              float* delta, int64_t batch, int64_t seq_len, int64_t h_q,
+                              int64_t head_dim, int dtype, void* stream) {
   using namespace moba;
   if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0)
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
@@ -590,8 +590,8 @@ extern "C" int moba_bwd_delta(const void* out, const void* dout, float* delta, i
     auto go = [&](auto lanes_c) {
       constexpr int Lc = decltype(lanes_c)::value;
       hipLaunchKernelGGL((delta_kernel<T, Lc>), grid, dim3(256), 0, as_stream(stream),
-                         static_cast<const T*>(out), static_cast<const T*>(dout), delta,
-                         n_rows, seq_len, h_q);
+                         static_cast<const T*>(out), static_cast<const T*>(dout), lse,
+                         delta, n_rows, seq_len, h_q);
     };
     switch (lanes) {
       case 1: go(std::integral_constant<int, 1>{}); break;
@@ -607,7 +607,7 @@ extern "C" int moba_bwd_delta(const void* out, const void* dout, float* delta, i
 }
 
 extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
-                        const float* lse, const float* delta, const int32_t* col_nnz,
+                        const float* lse_delta, const int32_t* col_nnz,
                         const int32_t* col_offsets, const int32_t* row_indices,
                         const int32_t* head_indices, const int32_t* slot_of_pair,
                         const int32_t* order, void* dk, void* dv, void* dq_part,
@@ -623,9 +623,9 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
                         slot_of_pair, order, cu_seqlens, batch, seq_len, max_seqlen, h_q,
                         h_kv, head_dim, n_blocks, block_size, slots, index_cap, causal);
   if (st) return st;
-  if (!dout || !lse || !delta || !dk || !dv || !dq_part)
+  if (!dout || !lse_delta || !dk || !dv || !dq_part)
     return fail(MOBA_ERR_INVALID, "null pointer");
-  a.dout = dout; a.lse = lse; a.delta = delta; a.dk = dk; a.dv = dv; a.part_acc = dq_part;
+  a.dout = dout; a.lse_delta = lse_delta; a.dk = dk; a.dv = dv; a.part_acc = dq_part;
   hipStream_t s = as_stream(stream);
   st = bwd_mfma(a, dtype, acc_dtype, batch * h_kv, s);
   if (st != MOBA_ERR_UNSUPPORTED) return st;
@@ -656,20 +656,23 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
   });
 }
 
-extern "C" int moba_dq_reduce(const void* dq_part, const float* part_m, void* dq,
+extern "C" int moba_dq_reduce(const void* dq_part, const float* part_m, int64_t m_stride,
+                              void* dq,
                               int64_t batch, int64_t seq_len, int64_t h_q, int64_t head_dim,
                               int64_t slots, int acc_dtype, int out_dtype, void* stream) {
   using namespace moba;
   if (batch <= 0 || seq_len <= 0 || h_q <= 0 || head_dim <= 0 || slots <= 0)
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
   if (!dq_part || !part_m || !dq) return fail(MOBA_ERR_INVALID, "null pointer");
+  if (m_stride < 1) return fail(MOBA_ERR_INVALID, "m_stride must be positive");
   if (head_dim % 8) return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
   const int64_t n_rows = batch * h_q * seq_len;
   dim3 grid(static_cast<unsigned>(cdiv(n_rows * (head_dim / 8), 256)));
   return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
     return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
       hipLaunchKernelGGL((dq_reduce_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
-                         static_cast<const A*>(dq_part), part_m, static_cast<O*>(dq), n_rows,
+                         static_cast<const A*>(dq_part), part_m, m_stride, static_cast<O*>(dq),
+                         n_rows,
                          seq_len, h_q, head_dim, slots);
       return check_launch("moba_dq_reduce");
     });

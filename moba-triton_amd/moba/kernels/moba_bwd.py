@@ -8,14 +8,24 @@ from moba.gqa import head_group_size
 from moba.kernels.routing import CSCIndex
 
 
-def compute_delta(out: torch.Tensor, dout: torch.Tensor) -> torch.Tensor:
-    """delta = rowsum(dO * O), [B, H, S] fp32 (`moba_bwd.py:454-470`)."""
+def compute_delta(out: torch.Tensor, dout: torch.Tensor, lse=None) -> torch.Tensor:
+    """delta = rowsum(dO * O), [B, H, S] fp32 (`moba_bwd.py:454-470`).
+
+    With `lse` [B, H, S] given, returns the (lse, delta) pairs [B, H, S, 2]
+    the backward kernel reads instead, one 8-byte record per row.
+    """
     b, s, h, d = out.shape
     dev = _lib.require_gpu(out, dout)
     out, dout = out.contiguous(), dout.to(out.dtype).contiguous()
-    delta = torch.empty((b, h, s), device=dev, dtype=torch.float32)
-    _lib.call("moba_bwd_delta", _lib.ptr(out), _lib.ptr(dout), _lib.ptr(delta),
-              b, s, h, d, _lib.DTYPE_CODE[out.dtype], _lib.stream_handle(dev))
+    if lse is not None:
+        if lse.shape != (b, h, s):
+            raise ValueError(f"lse {tuple(lse.shape)} does not match {(b, h, s)}")
+        lse = lse.float().contiguous()
+    shape = (b, h, s) if lse is None else (b, h, s, 2)
+    delta = torch.empty(shape, device=dev, dtype=torch.float32)
+    _lib.call("moba_bwd_delta", _lib.ptr(out), _lib.ptr(dout), _lib.ptr(lse),
+              _lib.ptr(delta), b, s, h, d, _lib.DTYPE_CODE[out.dtype],
+              _lib.stream_handle(dev))
     return delta
 
 
@@ -26,8 +36,12 @@ def reduce_dq(dq_part: torch.Tensor, part_m: torch.Tensor, out_dtype) -> torch.T
         raise ValueError(f"part_m {tuple(part_m.shape)} does not match dq_part "
                          f"{tuple(dq_part.shape)}")
     dev = _lib.require_gpu(dq_part, part_m)
+    m_stride = 2 if (part_m.dtype == torch.float32 and slots > 0 and
+                     part_m.stride() == (2 * h * s * slots, 2 * s * slots, 2 * slots, 2)) else 1
+    if m_stride == 1:
+        part_m = part_m.float().contiguous()
     dq = torch.empty((b, s, h, d), device=dev, dtype=out_dtype)
-    _lib.call("moba_dq_reduce", _lib.ptr(dq_part.contiguous()), _lib.ptr(part_m.contiguous()),
+    _lib.call("moba_dq_reduce", _lib.ptr(dq_part.contiguous()), _lib.ptr(part_m), m_stride,
               _lib.ptr(dq), b, s, h, d, slots, _lib.DTYPE_CODE[dq_part.dtype],
               _lib.DTYPE_CODE[out_dtype], _lib.stream_handle(dev))
     return dq
@@ -48,14 +62,14 @@ def moba_backward(dout, q, k, v, out, lse, part_m, cfg: MoBAConfig, index: CSCIn
     slots = index.max_slots
     q, k, v = (_lib.aligned_contiguous(t) for t in (q, k, v))
     dout = _lib.aligned_contiguous(dout.to(q.dtype))
-    delta = compute_delta(out, dout)
+    lse_delta = compute_delta(out, dout, lse)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     dq_part = torch.empty((b, h_q, s, slots, d), device=dev, dtype=q.dtype)
     rows = index.col_nnz.shape[0]
     mx = index.max_seqlen if index.cu_seqlens is not None else s
     _lib.call("moba_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(dout),
-              _lib.ptr(lse.contiguous()), _lib.ptr(delta), _lib.ptr(index.col_nnz),
+              _lib.ptr(lse_delta), _lib.ptr(index.col_nnz),
               _lib.ptr(index.col_offsets), _lib.ptr(index.row_indices),
               _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
               _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),

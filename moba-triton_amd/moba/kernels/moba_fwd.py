@@ -19,11 +19,41 @@ from moba.varlen import validate_cu_seqlens
 def empty_partials(shape, slots: int, device, partials_dtype=torch.float32):
     """Uninitialised head-major partial buffers for a token-major query
     shape (`moba_fwd.py:529-563`): part_m, part_l [B, H, S, K] fp32 and
-    part_acc [B, H, S, K, D] in `partials_dtype`."""
+    part_acc [B, H, S, K, D] in `partials_dtype`.
+
+    part_m and part_l are the two halves of one interleaved [B, H, S, K, 2]
+    buffer, so that a slot's (m, l) pair is one 8-byte record in HBM.
+    """
     b, s, h, d = shape
-    return (torch.empty((b, h, s, slots), device=device, dtype=torch.float32),
-            torch.empty((b, h, s, slots), device=device, dtype=torch.float32),
+    ml = torch.empty((b, h, s, slots, 2), device=device, dtype=torch.float32)
+    return (ml[..., 0], ml[..., 1],
             torch.empty((b, h, s, slots, d), device=device, dtype=partials_dtype))
+
+
+def _interleaved(part_m, part_l) -> bool:
+    """True when part_m / part_l are the halves of one (m, l) pair buffer
+    as `empty_partials` makes them."""
+    if part_m.dtype != torch.float32 or part_l.dtype != torch.float32:
+        return False
+    if part_m.shape != part_l.shape or part_m.stride() != part_l.stride():
+        return False
+    if part_l.data_ptr() != part_m.data_ptr() + 4:
+        return False
+    want, run = [], 2
+    for n in reversed(part_m.shape):
+        want.append(run)
+        run *= n
+    return all(st == w or n == 1 for st, w, n in
+               zip(part_m.stride(), reversed(want), part_m.shape))
+
+
+def pack_ml(part_m, part_l) -> torch.Tensor:
+    """The (m, l) pair buffer [..., 2] fp32 for the library: the shared base
+    of interleaved halves, else a packed copy."""
+    if _interleaved(part_m, part_l):
+        return torch.as_strided(part_m, tuple(part_m.shape) + (2,),
+                                tuple(part_m.stride()) + (1,))
+    return torch.stack((part_m.float(), part_l.float()), dim=-1).contiguous()
 
 
 def _rows(index: CSCIndex, b: int) -> int:
@@ -35,7 +65,8 @@ def attend_partials(q, k, v, cfg: MoBAConfig, index: CSCIndex, causal: bool = Tr
     """The attention stage, returning un-merged partials (`moba_fwd.py:566-665`).
 
     part_m is reset to -inf inside the library call (the written-marker);
-    part_l / part_acc of unwritten slots are never read.
+    part_l / part_acc of unwritten slots are never read. Caller-given
+    `partials` must come from `empty_partials` (interleaved m / l halves).
     """
     b, s, h_q, d = q.shape
     h_kv = k.shape[2]
@@ -46,6 +77,8 @@ def attend_partials(q, k, v, cfg: MoBAConfig, index: CSCIndex, causal: bool = Tr
     if partials is None:
         partials = empty_partials(q.shape, slots, dev, partials_dtype)
     part_m, part_l, part_acc = partials
+    if not _interleaved(part_m, part_l):
+        raise ValueError("partials must come from empty_partials (interleaved m / l)")
     q, k, v = (_lib.aligned_contiguous(t) for t in (q, k, v))
     rows = _rows(index, b)
     mx = index.max_seqlen if index.cu_seqlens is not None else s
@@ -53,8 +86,7 @@ def attend_partials(q, k, v, cfg: MoBAConfig, index: CSCIndex, causal: bool = Tr
               _lib.ptr(index.col_nnz), _lib.ptr(index.col_offsets),
               _lib.ptr(index.row_indices), _lib.ptr(index.head_indices),
               _lib.ptr(index.slot_of_pair), _lib.ptr(index.order),
-              _lib.ptr(part_m), _lib.ptr(part_l), _lib.ptr(part_acc),
-              _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d,
+              _lib.ptr(part_m), _lib.ptr(part_acc), _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d,
               index.num_blocks, cfg.block_size, slots, index.row_indices.shape[-1],
               int(bool(causal)), _lib.DTYPE_CODE[q.dtype],
               _lib.DTYPE_CODE[part_acc.dtype], _lib.stream_handle(dev))
@@ -82,12 +114,11 @@ def combine_partials(part_m, part_l, part_acc, out_dtype, block_m=None,
         raise ValueError(f"shape mismatch: part_acc {tuple(part_acc.shape)} against "
                          f"{(b, h, s, slots, d)}")
     dev = _lib.require_gpu(part_m, part_l, part_acc)
-    part_m, part_l, part_acc = (t.contiguous() for t in (part_m, part_l, part_acc))
-    if part_m.dtype != torch.float32 or part_l.dtype != torch.float32:
-        part_m, part_l = part_m.float(), part_l.float()
+    ml = pack_ml(part_m, part_l)
+    part_acc = part_acc.contiguous()
     out = torch.empty((b, s, h, d), device=dev, dtype=out_dtype)
     lse = torch.empty((b, h, s), device=dev, dtype=torch.float32) if return_lse else None
-    _lib.call("moba_combine", _lib.ptr(part_m), _lib.ptr(part_l), _lib.ptr(part_acc),
+    _lib.call("moba_combine", _lib.ptr(ml), _lib.ptr(part_acc),
               _lib.ptr(out), _lib.ptr(lse), b, s, h, d, slots,
               _lib.DTYPE_CODE[part_acc.dtype], _lib.DTYPE_CODE[out_dtype],
               _lib.stream_handle(dev))
