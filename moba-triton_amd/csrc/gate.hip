@@ -604,15 +604,19 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       cnt = 0;
       if (lv[M - 1] > -INFINITY) thr = fmaxf(thr0, lv[M - 1]);
     };
-    // A score is appended only when it beats the threshold; the wave-wide
-    // ballot skips the append for the (common) scores no lane keeps.
-    auto append = [&](float a, uint32_t id) {
-      const bool hit = a > thr;
-      if (__ballot(hit) != 0) {
-        if (hit) {
-          sv[cnt * 64] = a;
-          si[cnt * 64] = static_cast<uint16_t>(id);
-          ++cnt;
+    // Scores go in groups of four consecutive blocks. A group is skipped
+    // when no lane's group maximum beats its threshold (one wave-wide
+    // ballot); otherwise each score is written at the lane's next free entry
+    // and only a score that beats the threshold advances it (no per-score
+    // branch). The fold below keeps 16 free entries for every chunk.
+    auto append4 = [&](const float (&x)[4], uint32_t id0) {
+      const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      if (__ballot(mx > thr) != 0) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          sv[cnt * 64] = x[w];
+          si[cnt * 64] = static_cast<uint16_t>(id0 + w);
+          cnt += x[w] > thr ? 1 : 0;
         }
       }
     };
@@ -620,12 +624,19 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       const uint32_t base = static_cast<uint32_t>(ch * 32 + 4 * half);
       if (full) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) append(acc[v], base + 8 * (v >> 2) + (v & 3));
+        for (int g = 0; g < 4; ++g) {
+          const float x[4] = {acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+          append4(x, base + 8 * g);
+        }
       } else {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const uint32_t id = base + 8 * (v >> 2) + (v & 3);
-          append(static_cast<int>(id) < own ? acc[v] : -INFINITY, id);
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t id0 = base + 8 * g;
+          float x[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            x[w] = static_cast<int>(id0 + w) < own ? acc[4 * g + w] : -INFINITY;
+          append4(x, id0);
         }
       }
       if (__any(cnt > CAP - 16)) fold();
