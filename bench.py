@@ -133,7 +133,7 @@ def stage_times(s, dev, reps=5):
                   _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
                   _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),
                   None, 1, s, s, HEADS, HEADS, HEAD_DIM, index.num_blocks, BLOCK, TOPK,
-                  index.row_indices.shape[-1], 1, 0, 0, _lib.stream_handle(dev))
+                  index.row_indices.shape[-1], 3, 1, 0, 0, _lib.stream_handle(dev))
 
     st["bwd"] = timed(bwd, reps, 1)[0]
     st["dq_reduce"] = timed(lambda: reduce_dq(dq_part, parts[0], q.dtype), reps, 1)[0]

@@ -47,8 +47,9 @@ enum moba_status {
 
 enum moba_dtype { MOBA_BF16 = 0, MOBA_FP16 = 1, MOBA_FP32 = 2 };
 
-/* Library identity. moba_abi_version() is 2: (m, l) and (lse, delta) travel
- * as 8-byte pairs (version 1 took them as separate arrays). */
+/* Library identity. moba_abi_version() is 3: (m, l) and (lse, delta) travel
+ * as 8-byte pairs, and the CSC index arrays take an element stride (version
+ * 1 took separate statistics arrays; version 2 had no index stride). */
 int moba_abi_version(void);
 const char* moba_last_error(void);
 const char* moba_status_string(int status);
@@ -94,6 +95,10 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * an atomic cursor, so their order inside a column is unspecified (as in the
  * reference, routing.py:35-52); each (query, slot) pair appears exactly
  * once. row_indices hold packed token indices when cu_seqlens is given.
+ * Entry i of the three index arrays is element i * index_stride of each:
+ * index_stride 1 for three separate arrays, 3 for one array of (row, head,
+ * slot) records passed as base, base + 1, base + 2 (one record per entry
+ * keeps each scattered entry in one memory sector).
  * Replaces build_csc_from_indices (src/moba/kernels/routing.py:309-427)
  * and its three kernels (routing.py:139-301); CSCIndex fields of
  * routing.py:73-130.
@@ -107,7 +112,8 @@ int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                    int32_t* order, const int32_t* cu_seqlens, int64_t batch,
                    int64_t seq_len, int64_t max_seqlen, int64_t h_q,
                    int64_t h_kv, int64_t n_blocks, int64_t slots,
-                   void* workspace, size_t workspace_bytes, void* stream);
+                   int64_t index_stride, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /*
  * KV-block-major attend: for every column, the keys of that block against
@@ -116,7 +122,8 @@ int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
  * part_acc (sum of exp2 * v, in acc_dtype). m and l of a slot travel as
  * one 8-byte pair: part_ml [B, Hq, S, slots, 2] fp32 = (m, l); part_acc
  * [B, Hq, S, slots, D]. Unwritten slots keep m = -inf, which this call sets
- * before the kernel runs.
+ * before the kernel runs. The index arrays and index_stride are those of
+ * moba_csc_build.
  * Replaces attend_partials (src/moba/kernels/moba_fwd.py:566-665) and
  * moba_fwd_kernel (moba_fwd.py:230-425).
  */
@@ -128,8 +135,8 @@ int moba_attend(const void* q, const void* k, const void* v,
                 const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
                 int64_t max_seqlen, int64_t h_q, int64_t h_kv,
                 int64_t head_dim, int64_t n_blocks, int64_t block_size,
-                int64_t slots, int64_t index_cap, int causal, int dtype,
-                int acc_dtype, void* stream);
+                int64_t slots, int64_t index_cap, int64_t index_stride,
+                int causal, int dtype, int acc_dtype, void* stream);
 
 /*
  * LSE merge of the per-slot partials: out [B, S, Hq, D] (out_dtype) and,
@@ -161,7 +168,8 @@ int moba_bwd_delta(const void* out, const void* dout, const float* lse,
  * dq_part [B, Hq, S, slots, D] (acc_dtype). Replaces the kernel launch in
  * moba_backward (src/moba/kernels/moba_bwd.py:506-579; kernel
  * moba_bwd.py:216-394). lse_delta: the (lse, delta) pairs moba_bwd_delta
- * writes, lse in log2 units as moba_combine writes it.
+ * writes, lse in log2 units as moba_combine writes it. The index arrays and
+ * index_stride are those of moba_csc_build.
  */
 int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
              const float* lse_delta, const int32_t* col_nnz,
@@ -171,8 +179,8 @@ int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
              const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
              int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
              int64_t n_blocks, int64_t block_size, int64_t slots,
-             int64_t index_cap, int causal, int dtype, int acc_dtype,
-             void* stream);
+             int64_t index_cap, int64_t index_stride, int causal, int dtype,
+             int acc_dtype, void* stream);
 
 /*
  * dQ [B, S, Hq, D] = sum over written slots of dq_part, gated by the

@@ -17,6 +17,7 @@ struct AttnArgs {
   const int32_t* row_indices;
   const int32_t* head_indices;
   const int32_t* slot_of_pair;
+  int64_t istride;  // elements between consecutive entries of the three index arrays
   const int32_t* order;
   const int32_t* cu;
   float* part_ml;         // forward only: (m, l) per (row, slot)

@@ -136,9 +136,9 @@ attend_mfma_kernel(AttnArgs a) {
     // Unconditional loads (clamped entry) keep the wait counts static.
     const int32_t e = g + col;
     const int64_t i = c.lo + (e < c.n ? e : c.n - 1);
-    r = a.row_indices[i];
-    hd = a.head_indices[i];
-    sl = e < c.n ? a.slot_of_pair[i] : -1;
+    r = a.row_indices[i * a.istride];
+    hd = a.head_indices[i * a.istride];
+    sl = e < c.n ? a.slot_of_pair[i * a.istride] : -1;
   };
   u32x4 nq[CH];
   auto q_off = [&](int32_t r, int32_t hd, int32_t sl) -> int64_t {
@@ -447,9 +447,9 @@ bwd_mfma_kernel(AttnArgs a) {
   auto load_idx = [&](int32_t g) {
     const int32_t e = g + qi;
     const int64_t i = c.lo + (e < c.n ? e : last);
-    i_row = a.row_indices[i];
-    i_head = a.head_indices[i];
-    i_slot = e < c.n ? a.slot_of_pair[i] : -1;
+    i_row = a.row_indices[i * a.istride];
+    i_head = a.head_indices[i * a.istride];
+    i_slot = e < c.n ? a.slot_of_pair[i * a.istride] : -1;
   };
   int64_t n_pr = 0, n_dst = -1;                 // derived, step g + 1
   int n_lim = -1;

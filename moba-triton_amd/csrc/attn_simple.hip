@@ -67,9 +67,9 @@ attend_simple_kernel(AttnArgs a) {
     if (threadIdx.x < kE) {
       const int32_t e = e0 + threadIdx.x;
       const bool live = e < c.n;
-      Rs[threadIdx.x] = live ? a.row_indices[c.lo + e] : -1;
-      Hs[threadIdx.x] = live ? a.head_indices[c.lo + e] : 0;
-      Zs[threadIdx.x] = live ? a.slot_of_pair[c.lo + e] : 0;
+      Rs[threadIdx.x] = live ? a.row_indices[(c.lo + e) * a.istride] : -1;
+      Hs[threadIdx.x] = live ? a.head_indices[(c.lo + e) * a.istride] : 0;
+      Zs[threadIdx.x] = live ? a.slot_of_pair[(c.lo + e) * a.istride] : 0;
     }
     __syncthreads();
     for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
@@ -164,8 +164,8 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
     if (threadIdx.x < kBE) {
       const int32_t e = e0 + threadIdx.x;
       const bool live = e < c.n;
-      const int32_t row = live ? a.row_indices[c.lo + e] : -1;
-      const int32_t head = live ? a.head_indices[c.lo + e] : 0;
+      const int32_t row = live ? a.row_indices[(c.lo + e) * a.istride] : -1;
+      const int32_t head = live ? a.head_indices[(c.lo + e) * a.istride] : 0;
       Rs[threadIdx.x] = row;
       Hs[threadIdx.x] = head;
       Lse[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head)] : 0.f;
@@ -254,11 +254,11 @@ bwd_dq_simple_kernel(AttnArgs a) {
     if (threadIdx.x < kE) {
       const int32_t e = e0 + threadIdx.x;
       const bool live = e < c.n;
-      const int32_t row = live ? a.row_indices[c.lo + e] : -1;
-      const int32_t head = live ? a.head_indices[c.lo + e] : 0;
+      const int32_t row = live ? a.row_indices[(c.lo + e) * a.istride] : -1;
+      const int32_t head = live ? a.head_indices[(c.lo + e) * a.istride] : 0;
       Rs[threadIdx.x] = row;
       Hs[threadIdx.x] = head;
-      Zs[threadIdx.x] = live ? a.slot_of_pair[c.lo + e] : 0;
+      Zs[threadIdx.x] = live ? a.slot_of_pair[(c.lo + e) * a.istride] : 0;
       Lse[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head)] : 0.f;
       Dl[threadIdx.x] = live ? a.lse_delta[2 * part_row(a, c, row, head) + 1] : 0.f;
     }
@@ -457,7 +457,7 @@ static int prepare_attn(AttnArgs* a, Geometry* g, const void* q, const void* k,
                         const int32_t* cu, int64_t batch, int64_t seq_len,
                         int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
                         int64_t n_blocks, int64_t block_size, int64_t slots,
-                        int64_t index_cap, int causal) {
+                        int64_t index_cap, int64_t index_stride, int causal) {
   int st = make_geometry(g, batch, seq_len, max_seqlen, h_q, h_kv, head_dim, n_blocks,
                          block_size, slots, cu);
   if (st) return st;
@@ -467,12 +467,14 @@ static int prepare_attn(AttnArgs* a, Geometry* g, const void* q, const void* k,
   if (slots <= 0) return fail(MOBA_ERR_INVALID, "slots must be positive");
   if (index_cap < g->group * g->rows_per_seq * slots)
     return fail(MOBA_ERR_INVALID, "index capacity below group * rows * slots");
+  if (index_stride < 1) return fail(MOBA_ERR_INVALID, "index_stride must be positive");
   if (head_dim & (head_dim - 1))
     return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a power of two");
   *a = AttnArgs{};
   a->q = q; a->k = k; a->v = v;
   a->col_nnz = col_nnz; a->col_offsets = col_offsets; a->row_indices = row_indices;
   a->head_indices = head_indices; a->slot_of_pair = slot_of_pair; a->order = order;
+  a->istride = index_stride;
   a->cu = cu;
   a->S = seq_len; a->h_q = h_q; a->h_kv = h_kv; a->D = head_dim; a->n_blocks = n_blocks;
   a->bs = block_size; a->slots = slots; a->cap = index_cap; a->causal = causal ? 1 : 0;
@@ -516,14 +518,15 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
                            const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
                            int64_t max_seqlen, int64_t h_q, int64_t h_kv,
                            int64_t head_dim, int64_t n_blocks, int64_t block_size,
-                           int64_t slots, int64_t index_cap, int causal, int dtype,
-                           int acc_dtype, void* stream) {
+                           int64_t slots, int64_t index_cap, int64_t index_stride,
+                           int causal, int dtype, int acc_dtype, void* stream) {
   using namespace moba;
   AttnArgs a;
   Geometry g;
   int st = prepare_attn(&a, &g, q, k, v, col_nnz, col_offsets, row_indices, head_indices,
                         slot_of_pair, order, cu_seqlens, batch, seq_len, max_seqlen, h_q,
-                        h_kv, head_dim, n_blocks, block_size, slots, index_cap, causal);
+                        h_kv, head_dim, n_blocks, block_size, slots, index_cap,
+                        index_stride, causal);
   if (st) return st;
   if (!part_ml || !part_acc) return fail(MOBA_ERR_INVALID, "null partials");
   a.part_ml = part_ml; a.part_acc = part_acc;
@@ -614,14 +617,15 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
                         const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
                         int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
                         int64_t n_blocks, int64_t block_size, int64_t slots,
-                        int64_t index_cap, int causal, int dtype, int acc_dtype,
-                        void* stream) {
+                        int64_t index_cap, int64_t index_stride, int causal, int dtype,
+                        int acc_dtype, void* stream) {
   using namespace moba;
   AttnArgs a;
   Geometry g;
   int st = prepare_attn(&a, &g, q, k, v, col_nnz, col_offsets, row_indices, head_indices,
                         slot_of_pair, order, cu_seqlens, batch, seq_len, max_seqlen, h_q,
-                        h_kv, head_dim, n_blocks, block_size, slots, index_cap, causal);
+                        h_kv, head_dim, n_blocks, block_size, slots, index_cap,
+                        index_stride, causal);
   if (st) return st;
   if (!dout || !lse_delta || !dk || !dv || !dq_part)
     return fail(MOBA_ERR_INVALID, "null pointer");

@@ -31,7 +31,7 @@ count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __
                         int32_t* __restrict__ col_nnz_or_cursor,
                         const int32_t* __restrict__ col_offsets,
                         int32_t* __restrict__ row_indices, int32_t* __restrict__ head_indices,
-                        int32_t* __restrict__ slot_of_pair) {
+                        int32_t* __restrict__ slot_of_pair, int64_t istride) {
   const int64_t rh = blockIdx.y;
   const int64_t r = rh / h_q;
   const int64_t hq = rh % h_q;
@@ -49,26 +49,50 @@ count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __
   const int64_t colbase = (r * h_kv + hk) * n_blocks;
   const int32_t within = atomicAdd(&col_nnz_or_cursor[colbase + blk], 1);
   if (kScatter) {
-    const int64_t dst = (r * h_kv + hk) * cap +
-                        col_offsets[(r * h_kv + hk) * (n_blocks + 1) + blk] + within;
+    const int64_t dst = ((r * h_kv + hk) * cap +
+                         col_offsets[(r * h_kv + hk) * (n_blocks + 1) + blk] + within) * istride;
     row_indices[dst] = static_cast<int32_t>(packed ? tok : t);
     head_indices[dst] = static_cast<int32_t>(hq);
     slot_of_pair[dst] = j;
   }
 }
 
-// Workgroup-aggregated variant: 256 queries of one (row, query head) per
-// workgroup, one lane per query. Selections are first counted in an LDS
-// histogram over the blocks this tile can see, so the global counter of each
-// block is touched once per workgroup -- the own block, which every query of
-// a block selects, would otherwise take 128 serialised global atomics. The
-// scatter pass reserves each block's range with one global atomic and hands
-// out positions from LDS.
-constexpr int kTileQ = 256;
+// Workgroup-aggregated variant: kTileQ queries of one (row, query head) per
+// workgroup, kTileT threads each taking kTileQ / kTileT of them. Selections
+// are first counted in an LDS histogram over the blocks this tile can see,
+// so the global counter of each block is touched once per workgroup -- the
+// own block, which every query of a block selects, would otherwise take 128
+// serialised global atomics, and a past block picked by several queries of
+// the tile takes one. Those per-(tile, block) atomics bound both passes, so
+// the tile is large. The scatter pass reserves each block's range with one
+// global atomic and hands out positions from LDS.
+constexpr int kTileQ = 1024;
+typedef int32_t i32x3 __attribute__((ext_vector_type(3), aligned(4)));
+constexpr int kTileT = 256;
 constexpr int kMaxBins = 16384;
 
+// atomicAdd(&bins[blk], 1) for every active lane, with the lanes that share
+// the first active lane's id served by one atomic (every query of a block
+// selects its own block, so a wave's 64 consecutive queries usually agree
+// there); returns the old value plus the lane's rank among them.
+__device__ inline int32_t bin_add(int32_t* bins, int32_t blk, bool active) {
+  const uint64_t act = __ballot(active);
+  if (act == 0) return 0;
+  const int lead = __builtin_ctzll(act);
+  const int32_t b0 = __shfl(blk, lead);
+  const bool same = active && blk == b0;
+  const uint64_t m = __ballot(same);
+  const int lane = threadIdx.x & 63;
+  const int32_t rank = __popcll(m & ((uint64_t(1) << lane) - 1));
+  int32_t base = 0;
+  if (lane == lead) base = atomicAdd(&bins[b0], __popcll(m));
+  base = __shfl(base, lead);
+  if (same) return base + rank;
+  return active ? atomicAdd(&bins[blk], 1) : 0;
+}
+
 template <bool kScatter>
-__global__ void __launch_bounds__(kTileQ)
+__global__ void __launch_bounds__(kTileT)
 tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
                              const int32_t* __restrict__ cu, int64_t S, int64_t h_q,
                              int64_t h_kv, int64_t n_blocks, int64_t bs, int slots,
@@ -76,7 +100,8 @@ tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
                              const int32_t* __restrict__ col_offsets,
                              int32_t* __restrict__ row_indices,
                              int32_t* __restrict__ head_indices,
-                             int32_t* __restrict__ slot_of_pair) {
+                             int32_t* __restrict__ slot_of_pair, int64_t istride,
+                             bool records) {
   __shared__ int32_t bins[kMaxBins];
   const int64_t rh = blockIdx.y;
   const int64_t r = rh / h_q;
@@ -89,39 +114,55 @@ tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
   const int64_t t_last = (t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len) - 1;
   const int64_t nv = t_last / bs + 1;  // blocks any query here can select
   const int nvis = static_cast<int>(nv < n_blocks ? nv : n_blocks);
-  for (int b = threadIdx.x; b < nvis; b += kTileQ) bins[b] = 0;
+  for (int b = threadIdx.x; b < nvis; b += kTileT) bins[b] = 0;
   __syncthreads();
-  const int64_t t = t0 + threadIdx.x;
-  const bool live = t < sp.len;
-  const int64_t tok = sp.bos + t;
-  const int64_t qid = packed ? hq * S + tok : (r * h_q + hq) * S + t;
-  if (live)
+  // Query i of this thread: t0 + threadIdx.x + kTileT * i (a wave's lanes
+  // hold consecutive queries).
+  auto query = [&](int i, int64_t& t, int64_t& tok, int64_t& qid) {
+    t = t0 + threadIdx.x + kTileT * i;
+    tok = sp.bos + t;
+    qid = packed ? hq * S + tok : (r * h_q + hq) * S + t;
+    return t < sp.len;
+  };
+  for (int i = 0; i < kTileQ / kTileT; ++i) {
+    int64_t t, tok, qid;
+    const bool live = query(i, t, tok, qid);
     for (int j = 0; j < slots; ++j) {
-      const int32_t blk = block_idx[qid * slots + j];
-      if (blk >= 0) atomicAdd(&bins[blk], 1);
+      const int32_t blk = live ? block_idx[qid * slots + j] : -1;
+      bin_add(bins, blk, blk >= 0);
     }
+  }
   __syncthreads();
   const int64_t colbase = (r * h_kv + hk) * n_blocks;
-  for (int b = threadIdx.x; b < nvis; b += kTileQ) {
+  const int64_t obase = (r * h_kv + hk) * (n_blocks + 1);
+  for (int b = threadIdx.x; b < nvis; b += kTileT) {
     const int32_t n = bins[b];
     if (n > 0) {
       const int32_t base = atomicAdd(&col_nnz_or_cursor[colbase + b], n);
-      if (kScatter) bins[b] = base;
+      // The scatter hands out positions from the column's start directly.
+      if (kScatter) bins[b] = col_offsets[obase + b] + base;
     }
   }
   if (!kScatter) return;
   __syncthreads();
-  if (!live) return;
-  const int64_t obase = (r * h_kv + hk) * (n_blocks + 1);
   const int64_t ibase = (r * h_kv + hk) * cap;
-  for (int j = 0; j < slots; ++j) {
-    const int32_t blk = block_idx[qid * slots + j];
-    if (blk < 0) continue;
-    const int32_t within = atomicAdd(&bins[blk], 1);
-    const int64_t dst = ibase + col_offsets[obase + blk] + within;
-    row_indices[dst] = static_cast<int32_t>(packed ? tok : t);
-    head_indices[dst] = static_cast<int32_t>(hq);
-    slot_of_pair[dst] = j;
+  for (int i = 0; i < kTileQ / kTileT; ++i) {
+    int64_t t, tok, qid;
+    const bool live = query(i, t, tok, qid);
+    for (int j = 0; j < slots; ++j) {
+      const int32_t blk = live ? block_idx[qid * slots + j] : -1;
+      const int32_t pos = bin_add(bins, blk, blk >= 0);
+      if (blk < 0) continue;
+      const int64_t dst = (ibase + pos) * istride;
+      const int32_t rv = static_cast<int32_t>(packed ? tok : t);
+      if (records) {  // (row, head, slot) adjacent: one 12-byte store
+        *reinterpret_cast<i32x3*>(row_indices + dst) = i32x3{rv, static_cast<int32_t>(hq), j};
+      } else {
+        row_indices[dst] = rv;
+        head_indices[dst] = static_cast<int32_t>(hq);
+        slot_of_pair[dst] = j;
+      }
+    }
   }
 }
 
@@ -199,7 +240,8 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                               int32_t* order, const int32_t* cu_seqlens, int64_t batch,
                               int64_t seq_len, int64_t max_seqlen, int64_t h_q,
                               int64_t h_kv, int64_t n_blocks, int64_t slots,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+                              int64_t index_stride, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   using namespace moba;
   Geometry g;
   const int64_t rps = cu_seqlens ? max_seqlen : seq_len;
@@ -207,6 +249,7 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                          n_blocks > 0 ? cdiv(rps, n_blocks) : 1, slots, cu_seqlens);
   if (st) return st;
   if (slots <= 0) return fail(MOBA_ERR_INVALID, "slots must be positive");
+  if (index_stride < 1) return fail(MOBA_ERR_INVALID, "index_stride must be positive");
   if (!block_idx || !col_nnz || !col_offsets || !row_indices || !head_indices ||
       !slot_of_pair || !order)
     return fail(MOBA_ERR_INVALID, "null pointer");
@@ -218,6 +261,8 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
     return fail(MOBA_ERR_UNSUPPORTED, "column capacity exceeds int32 offsets");
   hipStream_t s = as_stream(stream);
   int32_t* cursor = static_cast<int32_t*>(workspace);
+  const bool records = index_stride == 3 && head_indices == row_indices + 1 &&
+                       slot_of_pair == row_indices + 2;
   const int64_t ncols = batch * h_kv * n_blocks;
   const unsigned fill_blocks = static_cast<unsigned>(cdiv(ncols, 256) < 4096 ? cdiv(ncols, 256) : 4096);
   hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, col_nnz, ncols, 0);
@@ -231,15 +276,15 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   dim3 tgrid(static_cast<unsigned>(cdiv(g.rows_per_seq, kTileQ)),
              static_cast<unsigned>(batch * h_q));
   if (tiled)
-    hipLaunchKernelGGL(tile_count_or_scatter_kernel<false>, tgrid, dim3(kTileQ), 0, s,
+    hipLaunchKernelGGL(tile_count_or_scatter_kernel<false>, tgrid, dim3(kTileT), 0, s,
                        block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
                        static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
-                       nullptr);
+                       nullptr, index_stride, false);
   else
     hipLaunchKernelGGL(count_or_scatter_kernel<false>, grid, dim3(256), 0, s, block_idx,
                        cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
                        static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
-                       nullptr);
+                       nullptr, index_stride);
   hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024), 0, s,
                      col_nnz, col_offsets, n_blocks);
   hipLaunchKernelGGL(order_kernel,
@@ -247,14 +292,14 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                           static_cast<unsigned>(batch * h_kv)),
                      dim3(256), 0, s, col_nnz, order, n_blocks);
   if (tiled)
-    hipLaunchKernelGGL(tile_count_or_scatter_kernel<true>, tgrid, dim3(kTileQ), 0, s,
+    hipLaunchKernelGGL(tile_count_or_scatter_kernel<true>, tgrid, dim3(kTileT), 0, s,
                        block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
                        static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
-                       head_indices, slot_of_pair);
+                       head_indices, slot_of_pair, index_stride, records);
   else
     hipLaunchKernelGGL(count_or_scatter_kernel<true>, grid, dim3(256), 0, s, block_idx,
                        cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
                        static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
-                       head_indices, slot_of_pair);
+                       head_indices, slot_of_pair, index_stride);
   return check_launch("moba_csc_build");
 }

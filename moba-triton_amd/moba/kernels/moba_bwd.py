@@ -5,7 +5,7 @@ import torch
 from moba import _lib
 from moba.config import MoBAConfig
 from moba.gqa import head_group_size
-from moba.kernels.routing import CSCIndex
+from moba.kernels.routing import CSCIndex, index_stride
 
 
 def compute_delta(out: torch.Tensor, dout: torch.Tensor, lse=None) -> torch.Tensor:
@@ -74,7 +74,8 @@ def moba_backward(dout, q, k, v, out, lse, part_m, cfg: MoBAConfig, index: CSCIn
               _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
               _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),
               _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d, index.num_blocks,
-              cfg.block_size, slots, index.row_indices.shape[-1], int(bool(causal)),
+              cfg.block_size, slots, index.row_indices.shape[-1], index_stride(index),
+              int(bool(causal)),
               _lib.DTYPE_CODE[q.dtype], _lib.DTYPE_CODE[dq_part.dtype],
               _lib.stream_handle(dev))
     return reduce_dq(dq_part, part_m, q.dtype), dk, dv

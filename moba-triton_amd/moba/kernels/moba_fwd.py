@@ -12,7 +12,7 @@ from moba import _lib
 from moba.config import MoBAConfig
 from moba.device import TENSOR_CORE_TILE, check_gathered_head_dim
 from moba.gqa import head_group_size
-from moba.kernels.routing import CSCIndex, build_csc_fused
+from moba.kernels.routing import CSCIndex, build_csc_fused, index_stride
 from moba.varlen import validate_cu_seqlens
 
 
@@ -88,7 +88,7 @@ def attend_partials(q, k, v, cfg: MoBAConfig, index: CSCIndex, causal: bool = Tr
               _lib.ptr(index.slot_of_pair), _lib.ptr(index.order),
               _lib.ptr(part_m), _lib.ptr(part_acc), _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d,
               index.num_blocks, cfg.block_size, slots, index.row_indices.shape[-1],
-              int(bool(causal)), _lib.DTYPE_CODE[q.dtype],
+              index_stride(index), int(bool(causal)), _lib.DTYPE_CODE[q.dtype],
               _lib.DTYPE_CODE[part_acc.dtype], _lib.stream_handle(dev))
     return part_m, part_l, part_acc
 

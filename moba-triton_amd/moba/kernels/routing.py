@@ -45,6 +45,29 @@ class CSCIndex:
     max_seqlen: int | None = None
 
 
+def index_stride(index: CSCIndex) -> int:
+    """Element stride shared by the three index arrays (3 for the record
+    layout `build_csc_from_indices` makes, 1 for separate arrays).
+
+    Raises:
+        ValueError: If the arrays differ in dtype, shape or strides, or are
+            not uniformly strided over (row, kv head, entry).
+    """
+    fields = (index.row_indices, index.head_indices, index.slot_of_pair)
+    if any(t.dtype != torch.int32 for t in fields):
+        raise ValueError("index arrays must be int32")
+    if len({tuple(t.shape) for t in fields}) != 1 or len({t.stride() for t in fields}) != 1:
+        raise ValueError("row_indices, head_indices and slot_of_pair must share shape and strides")
+    shape, st = fields[0].shape, fields[0].stride()
+    step = st[-1]
+    run = step
+    for n, s_ in zip(reversed(shape), reversed(st)):
+        if n != 1 and s_ != run:
+            raise ValueError("index arrays must be uniformly strided over (row, kv head, entry)")
+        run *= n
+    return int(step)
+
+
 def build_csc_from_indices(block_idx: torch.Tensor, num_blocks: int, cfg: MoBAConfig,
                            num_kv_heads: int | None = None,
                            cu_seqlens: torch.Tensor | None = None,
@@ -78,16 +101,17 @@ def build_csc_from_indices(block_idx: torch.Tensor, num_blocks: int, cfg: MoBACo
     col_nnz = torch.empty(rows, h_kv, num_blocks, **i32)
     col_offsets = torch.empty(rows, h_kv, num_blocks + 1, **i32)
     order = torch.empty(rows, h_kv, num_blocks, **i32)
-    row_indices = torch.empty(rows, h_kv, cap, **i32)
-    head_indices = torch.empty(rows, h_kv, cap, **i32)
-    slot_of_pair = torch.empty(rows, h_kv, cap, **i32)
+    # One (row, head, slot) record per entry: the scatter writes each entry
+    # into one memory sector. The three fields are strided views of it.
+    entries = torch.empty(rows, h_kv, cap, 3, **i32)
+    row_indices, head_indices, slot_of_pair = entries.unbind(-1)
     lib = _lib.load()
     ws_bytes = int(lib.moba_csc_workspace_size(rows, s, h_q, h_kv, num_blocks, slots))
     ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
     _lib.call("moba_csc_build", _lib.ptr(block_idx), _lib.ptr(col_nnz),
               _lib.ptr(col_offsets), _lib.ptr(row_indices), _lib.ptr(head_indices),
               _lib.ptr(slot_of_pair), _lib.ptr(order), _lib.ptr(cu_seqlens), rows, s,
-              rps, h_q, h_kv, num_blocks, slots, _lib.ptr(ws), ws.numel(),
+              rps, h_q, h_kv, num_blocks, slots, 3, _lib.ptr(ws), ws.numel(),
               _lib.stream_handle(dev))
     return CSCIndex(col_nnz=col_nnz, col_offsets=col_offsets, row_indices=row_indices,
                     head_indices=head_indices, slot_of_pair=slot_of_pair, order=order,

@@ -96,3 +96,32 @@ def test_no_cpu_fallback():
     q = torch.zeros(1, 256, 4, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="GPU"):
         moba_forward(q, q, q, cfg)
+
+
+def test_index_stride_layouts():
+    """The index arrays reach the library as (base pointer, element stride):
+    3 for the (row, head, slot) records the CSC build makes, 1 for three
+    separate arrays; anything else is refused before a launch."""
+    from moba.kernels.routing import CSCIndex, index_stride
+
+    def make(rows, heads, slots):
+        z = torch.zeros(1, 2, 8, dtype=torch.int32)
+        return CSCIndex(col_nnz=z, col_offsets=z, row_indices=rows, head_indices=heads,
+                        slot_of_pair=slots, order=z, num_blocks=8, max_slots=2,
+                        num_query_heads=2)
+
+    rec = torch.zeros(1, 2, 16, 3, dtype=torch.int32)
+    r, h, s = rec.unbind(-1)
+    assert index_stride(make(r, h, s)) == 3
+    assert h.data_ptr() - r.data_ptr() == 4 and s.data_ptr() - r.data_ptr() == 8
+    sep = [torch.zeros(1, 2, 16, dtype=torch.int32) for _ in range(3)]
+    assert index_stride(make(*sep)) == 1
+    with pytest.raises(ValueError):
+        index_stride(make(r, sep[1], sep[2]))           # mixed strides
+    with pytest.raises(ValueError):
+        index_stride(make(*(t.long() for t in sep)))   # wrong dtype
+    wide = [torch.zeros(1, 2, 20, dtype=torch.int32)[:, :, :16] for _ in range(3)]
+    with pytest.raises(ValueError):
+        index_stride(make(*wide))                      # padding between kv heads
+    even = [t[:, :, ::2] for t in sep]                 # uniform stride 2 is fine
+    assert index_stride(make(*even)) == 2
