@@ -354,7 +354,12 @@ __device__ inline void store8<float>(float* p, const float (&x)[8]) {
 
 // One lane per (query, 8 features). Two passes over the slots, as in the
 // reference merge: the global max, then the rescaled sums.
-template <typename A, typename O>
+// One lane per (query, 8 features). K > 0 fixes the slot count at compile
+// time: every slot's partial row is then requested before the first is
+// used (the addresses are valid whether or not the slot was written, and an
+// unwritten slot's values are selected away, never multiplied in), so a lane
+// keeps K loads in flight. K = 0 loops over `slots` at run time.
+template <typename A, typename O, int K>
 __global__ void __launch_bounds__(256)
 combine_kernel(const float* __restrict__ part_ml, const A* __restrict__ part_acc, O* __restrict__ out, float* __restrict__ lse,
                int64_t n_rows, int64_t S, int64_t h_q, int64_t D, int64_t slots) {
@@ -365,18 +370,38 @@ combine_kernel(const float* __restrict__ part_ml, const A* __restrict__ part_acc
   if (row >= n_rows) return;
   const float* ml = part_ml + row * slots * 2;  // (m, l) per slot
   float m_g = -INFINITY;
-  for (int64_t j = 0; j < slots; ++j) m_g = fmaxf(m_g, ml[2 * j]);
   float ls = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int64_t j = 0; j < slots; ++j) {
-    const float mi = ml[2 * j];
-    if (mi > -INFINITY) {
-      const float w = exp2f(mi - m_g);
-      ls += ml[2 * j + 1] * w;
-      float x[8];
-      load8<A>(part_acc + (row * slots + j) * D + d0, x);
+  if constexpr (K > 0) {
+    float2 st[K];
+    float x[K][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += x[i] * w;
+    for (int j = 0; j < K; ++j) {
+      st[j] = *reinterpret_cast<const float2*>(ml + 2 * j);
+      load8<A>(part_acc + (row * K + j) * D + d0, x[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) m_g = fmaxf(m_g, st[j].x);
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const bool ok = st[j].x > -INFINITY;
+      const float w = ok ? exp2f(st[j].x - m_g) : 0.f;
+      ls += ok ? st[j].y * w : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += (ok ? x[j][i] : 0.f) * w;
+    }
+  } else {
+    for (int64_t j = 0; j < slots; ++j) m_g = fmaxf(m_g, ml[2 * j]);
+    for (int64_t j = 0; j < slots; ++j) {
+      const float mi = ml[2 * j];
+      if (mi > -INFINITY) {
+        const float w = exp2f(mi - m_g);
+        ls += ml[2 * j + 1] * w;
+        float x[8];
+        load8<A>(part_acc + (row * slots + j) * D + d0, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += x[i] * w;
+      }
     }
   }
 #pragma unroll
@@ -416,8 +441,11 @@ delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, const float* _
 }
 
 // One lane per (query, 8 features); a slot counts only if the forward wrote
-// it (part_m > -inf), so unwritten dq partials are never read.
-template <typename A, typename O>
+// it (part_m > -inf), so unwritten dq partials never reach the sum. K as in
+// combine_kernel: with K > 0 every slot's row is requested up front (and an
+// unwritten slot's values selected away); K = 0 loops at run time and
+// reads only the written slots.
+template <typename A, typename O, int K>
 __global__ void __launch_bounds__(256)
 dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m,
                  int64_t m_stride, O* __restrict__ dq, int64_t n_rows, int64_t S,
@@ -428,13 +456,29 @@ dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m
   const int64_t d0 = (gid % per_row) * 8;
   if (row >= n_rows) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int64_t j = 0; j < slots; ++j)
-    if (part_m[(row * slots + j) * m_stride] > -INFINITY) {
-      float x[8];
-      load8<A>(dq_part + (row * slots + j) * D + d0, x);
+  if constexpr (K > 0) {
+    float mk[K];
+    float x[K][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += x[i];
+    for (int j = 0; j < K; ++j) {
+      mk[j] = part_m[(row * K + j) * m_stride];
+      load8<A>(dq_part + (row * K + j) * D + d0, x[j]);
     }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const bool ok = mk[j] > -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += ok ? x[j][i] : 0.f;
+    }
+  } else {
+    for (int64_t j = 0; j < slots; ++j)
+      if (part_m[(row * slots + j) * m_stride] > -INFINITY) {
+        float x[8];
+        load8<A>(dq_part + (row * slots + j) * D + d0, x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += x[i];
+      }
+  }
   const int64_t bh = row / S, t = row % S;
   const int64_t b = bh / h_q, h = bh % h_q;
   store8<O>(dq + ((b * S + t) * h_q + h) * D + d0, acc);
@@ -569,9 +613,14 @@ extern "C" int moba_combine(const float* part_ml, const void* part_acc,
   dim3 grid(static_cast<unsigned>(cdiv(n_rows * (head_dim / 8), 256)));
   return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
     return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
-      hipLaunchKernelGGL((combine_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
-                         part_ml, static_cast<const A*>(part_acc), static_cast<O*>(out),
-                         lse, n_rows, seq_len, h_q, head_dim, slots);
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, as_stream(stream), part_ml,
+                           static_cast<const A*>(part_acc), static_cast<O*>(out), lse, n_rows,
+                           seq_len, h_q, head_dim, slots);
+      };
+      if (slots == 8) go(combine_kernel<A, O, 8>);
+      else if (slots == 16) go(combine_kernel<A, O, 16>);
+      else go(combine_kernel<A, O, 0>);
       return check_launch("moba_combine");
     });
   });
@@ -674,10 +723,14 @@ extern "C" int moba_dq_reduce(const void* dq_part, const float* part_m, int64_t 
   dim3 grid(static_cast<unsigned>(cdiv(n_rows * (head_dim / 8), 256)));
   return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
     return MOBA_DISPATCH_DTYPE(out_dtype, O, [&] {
-      hipLaunchKernelGGL((dq_reduce_kernel<A, O>), grid, dim3(256), 0, as_stream(stream),
-                         static_cast<const A*>(dq_part), part_m, m_stride, static_cast<O*>(dq),
-                         n_rows,
-                         seq_len, h_q, head_dim, slots);
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, as_stream(stream),
+                           static_cast<const A*>(dq_part), part_m, m_stride,
+                           static_cast<O*>(dq), n_rows, seq_len, h_q, head_dim, slots);
+      };
+      if (slots == 8) go(dq_reduce_kernel<A, O, 8>);
+      else if (slots == 16) go(dq_reduce_kernel<A, O, 16>);
+      else go(dq_reduce_kernel<A, O, 0>);
       return check_launch("moba_dq_reduce");
     });
   });
