@@ -102,24 +102,6 @@ attend_mfma_kernel(AttnArgs a) {
   const uint16_t* Vg = static_cast<const uint16_t*>(a.v);
   const uint16_t* Q = static_cast<const uint16_t*>(a.q);
 
-  // Stage K (row-major) and V^T (permuted keys); tail keys are zero.
-  for (int i = tid; i < BS * D / 8; i += 256) {
-    const int key = i / (D / 8);
-    const int d8 = (i % (D / 8)) * 8;
-    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-    if (c.key0 + key < c.key_end) {
-      const int64_t off = ((c.tok0 + key) * a.h_kv + c.hk) * D + d8;
-      kv = *reinterpret_cast<const uint4*>(K + off);
-      vv = *reinterpret_cast<const uint4*>(Vg + off);
-    }
-    *reinterpret_cast<uint4*>(&Ks[key * KS + d8]) = kv;
-    const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
-    const int kp = (key & ~15) + perm16(key & 15);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) Vt[(d8 + u) * VS + kp] = ve[u];
-  }
-  __syncthreads();
-
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int h = lane >> 5;
@@ -145,17 +127,50 @@ attend_mfma_kernel(AttnArgs a) {
     return sl >= 0 ? q_offset(a, c, r, hd) : -1;
   };
   auto fetch = [&](int64_t off) {
+    // Unconditional: a dead entry reads row 0; its lanes' results are never
+    // stored, and every MFMA column (query) is independent of the others.
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int64_t o = __shfl(off, lane / RQ + (64 / RQ) * u);
-      nq[u] = u32x4{0, 0, 0, 0};
-      if (o >= 0) nq[u] = *reinterpret_cast<const u32x4*>(Q + o + (lane % RQ) * 8);
+      nq[u] = *reinterpret_cast<const u32x4*>(Q + (o >= 0 ? o : 0) + (lane % RQ) * 8);
     }
   };
+  // Column start: the first group's index entries and every K / V chunk of
+  // the block are requested together, the first group's Q rows as soon as
+  // its entries are in, and only then are K and V^T (permuted keys) written
+  // to LDS -- one memory round trip before the first group, not several.
+  constexpr int KVN = BS * D / 8 / 256;  // 16-byte K (and V) chunks per thread
+  static_assert(BS * D / 8 % 256 == 0, "K / V chunks must tile the workgroup");
   int32_t cr, chd, csl, nr, nhd, nsl;
   load_idx(wave * 32, cr, chd, csl);
+  u32x4 kc[KVN], vc[KVN];
+#pragma unroll
+  for (int u = 0; u < KVN; ++u) {
+    const int i = tid + u * 256;
+    const int key = i / (D / 8);
+    const int d8 = (i % (D / 8)) * 8;
+    const int kk = c.key0 + key < c.key_end ? key : 0;  // tail keys: a valid row, zeroed below
+    const int64_t off = ((c.tok0 + kk) * a.h_kv + c.hk) * D + d8;
+    kc[u] = *reinterpret_cast<const u32x4*>(K + off);
+    vc[u] = *reinterpret_cast<const u32x4*>(Vg + off);
+  }
   fetch(q_off(cr, chd, csl));
   load_idx(wave * 32 + 128, nr, nhd, nsl);
+#pragma unroll
+  for (int u = 0; u < KVN; ++u) {
+    const int i = tid + u * 256;
+    const int key = i / (D / 8);
+    const int d8 = (i % (D / 8)) * 8;
+    const bool kin = c.key0 + key < c.key_end;
+    const u32x4 kv = kin ? kc[u] : u32x4{0, 0, 0, 0};
+    const u32x4 vv = kin ? vc[u] : u32x4{0, 0, 0, 0};
+    *reinterpret_cast<u32x4*>(&Ks[key * KS + d8]) = kv;
+    const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
+    const int kp = (key & ~15) + perm16(key & 15);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) Vt[(d8 + w) * VS + kp] = ve[w];
+  }
+  __syncthreads();
   auto stage_q = [&]() {
 #pragma unroll
     for (int u = 0; u < CH; ++u)
@@ -401,34 +416,11 @@ bwd_mfma_kernel(AttnArgs a) {
   const uint16_t* Og = static_cast<const uint16_t*>(a.dout);
   const int key_lim = static_cast<int>(c.key_end - c.key0);
 
-  // K^T of the block in LDS (for dQ); K and V rows of this lane's key stay
-  // in registers as the B operands of S and dP for the whole column.
-  for (int i = tid; i < BS * D / 8; i += NT) {
-    const int key = i / (D / 8);
-    const int d8 = (i % (D / 8)) * 8;
-    uint4 kv = make_uint4(0, 0, 0, 0);
-    if (key < key_lim)
-      kv = *reinterpret_cast<const uint4*>(Kg + ((c.tok0 + key) * a.h_kv + c.hk) * D + d8);
-    const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kv);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) Kt[(d8 + u) * KTS + key] = ke[u];
-  }
-
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int h = lane >> 5;
   const int col = lane & 31;
   const int mykey = wave * 32 + col;  // the key this lane holds in S / dP / dV / dK
-  V8 kb[D / 16], vb[D / 16];
-  {
-    const bool kok = mykey < key_lim;
-    const int64_t off = ((c.tok0 + mykey) * a.h_kv + c.hk) * D + 8 * h;
-#pragma unroll
-    for (int k = 0; k < D / 16; ++k) {
-      kb[k] = kok ? ld16<V8>(Kg + off + 16 * k) : V8{};
-      vb[k] = kok ? ld16<V8>(Vg + off + 16 * k) : V8{};
-    }
-  }
   floatx16_t dv[DT], dk[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
@@ -484,12 +476,50 @@ bwd_mfma_kernel(AttnArgs a) {
   int c_lim = -1;
   int64_t c_dst = -1;
   float c_lse = 0.f, c_dl = 0.f;
+  // Column start: step 0's index entries, the block's K chunks for K^T in
+  // LDS (for dQ) and this lane's K and V rows (the B operands of S and dP
+  // for the whole column) are requested together; step 0's rows as soon as
+  // its entries are in; then K^T is written. Loads are unconditional: keys
+  // past the block's end read a valid row (K^T zeroes them; their S and dP
+  // are masked and their dK / dV never stored).
+  constexpr int KTN = BS * D / 8 / NT;  // 16-byte K chunks per thread for K^T
+  static_assert(BS * D / 8 % NT == 0, "K chunks must tile the workgroup");
+  if (c.n > 0) load_idx(0);
+  u32x4 ktc[KTN];
+#pragma unroll
+  for (int u = 0; u < KTN; ++u) {
+    const int i = tid + u * NT;
+    const int key = i / (D / 8);
+    const int d8 = (i % (D / 8)) * 8;
+    ktc[u] = *reinterpret_cast<const u32x4*>(
+        Kg + ((c.tok0 + (key < key_lim ? key : 0)) * a.h_kv + c.hk) * D + d8);
+  }
+  V8 kb[D / 16], vb[D / 16];
+  {
+    const int64_t off = ((c.tok0 + (mykey < key_lim ? mykey : 0)) * a.h_kv + c.hk) * D + 8 * h;
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) {
+      kb[k] = ld16<V8>(Kg + off + 16 * k);
+      vb[k] = ld16<V8>(Vg + off + 16 * k);
+    }
+  }
   if (c.n > 0) {
-    load_idx(0);
     derive();
     __syncthreads();
     fetch();
     load_idx(NQ);
+  }
+#pragma unroll
+  for (int u = 0; u < KTN; ++u) {
+    const int i = tid + u * NT;
+    const int key = i / (D / 8);
+    const int d8 = (i % (D / 8)) * 8;
+    const u32x4 kv = key < key_lim ? ktc[u] : u32x4{0, 0, 0, 0};
+    const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kv);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) Kt[(d8 + w) * KTS + key] = ke[w];
+  }
+  if (c.n > 0) {
     c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
     derive();  // s_qoff now describes step 1; every thread read step 0's above
   }
@@ -519,10 +549,16 @@ bwd_mfma_kernel(AttnArgs a) {
       const uint16_t* qe = reinterpret_cast<const uint16_t*>(&vq);
       const uint16_t* oe = reinterpret_cast<const uint16_t*>(&vo);
       const int qp = (q & ~15) + perm16(q & 15);
+      // Rows d8 .. d8 + 7 share d8's swizzle (d8 is a multiple of 8), so the
+      // eight writes are one base plus immediate offsets.
+      int tb = tq(d8, qp);
+      // Opaque to loop-invariant hoisting: otherwise each of the 16 row
+      // addresses is hoisted into a register of its own for the whole column.
+      asm volatile("" : "+v"(tb));
 #pragma unroll
       for (int w = 0; w < 8; ++w) {
-        Qt[tq(d8 + w, qp)] = qe[w];
-        Ot[tq(d8 + w, qp)] = oe[w];
+        Qt[tb + w * QTS] = qe[w];
+        Ot[tb + w * QTS] = oe[w];
       }
     }
     __syncthreads();
