@@ -140,6 +140,28 @@ def stage_times(s, dev, reps=5):
     return st
 
 
+def attainment(q, k, v, cfg, s, fwd_ms):
+    """The reference's headline ratio (`bench/suite.py:1-12, 549-583`): the
+    forward speedup over dense causal attention (torch SDPA, fused kernels
+    only, via the `sdpa_dense` backend) divided by the speedup the sparsity
+    pattern makes available (1 / `sparsity_ratio`)."""
+    from implementations import get_backend
+    from moba.sparsity import sparsity_ratio
+
+    ceiling = 1.0 / sparsity_ratio(s, cfg)
+    out = {"speedup_ceiling": round(ceiling, 2), "dense_fwd_ms": None,
+           "speedup_vs_dense_fwd": None, "attainment_fwd": None}
+    dense = get_backend("sdpa_dense")
+    try:
+        ms = timed(lambda: dense.forward(q, k, v, cfg), 2 if s >= 262144 else 5, 1)[0]
+    except RuntimeError as exc:
+        out["dense_note"] = str(exc)[:120]
+        return out
+    out.update(dense_fwd_ms=round(ms, 3), speedup_vs_dense_fwd=round(ms / fwd_ms, 2),
+               attainment_fwd=round(ms / fwd_ms / ceiling, 4))
+    return out
+
+
 def sweep(dev, seqs, reps=5):
     from moba.config import MoBAConfig
     from moba.kernels.attention import moba_attention
@@ -157,12 +179,14 @@ def sweep(dev, seqs, reps=5):
             moba_attention(qq, kk, vv, cfg).backward(do)
 
         fb = timed(step, reps, 2)[0]
-        rows.append({"seq_len": s, "fwd_ms": round(fwd, 4), "fwd_bwd_ms": round(fb, 4),
-                     "h100_ref_fwd_ms": H100_FWD_MS.get(s),
-                     "h100_ref_fwd_bwd_ms": H100_FWDBWD_MS.get(s),
-                     "speedup_fwd": round(H100_FWD_MS[s] / fwd, 2) if s in H100_FWD_MS else None,
-                     "speedup_fwd_bwd": round(H100_FWDBWD_MS[s] / fb, 2)
-                     if s in H100_FWDBWD_MS else None})
+        row = {"seq_len": s, "fwd_ms": round(fwd, 4), "fwd_bwd_ms": round(fb, 4),
+               "h100_ref_fwd_ms": H100_FWD_MS.get(s),
+               "h100_ref_fwd_bwd_ms": H100_FWDBWD_MS.get(s),
+               "speedup_fwd": round(H100_FWD_MS[s] / fwd, 2) if s in H100_FWD_MS else None,
+               "speedup_fwd_bwd": round(H100_FWDBWD_MS[s] / fb, 2)
+               if s in H100_FWDBWD_MS else None}
+        row.update(attainment(q, k, v, cfg, s, fwd))
+        rows.append(row)
         del q, k, v, do, qq, kk, vv
         torch.cuda.empty_cache()
     return rows

@@ -42,7 +42,8 @@ def test_head_group_and_expand():
 
 def test_registry_contract():
     names = [b.name for b in implementations.all_backends()]
-    assert "ours" in names and "triton_moba" in names
+    assert "ours" in names and "triton_moba" in names and "sdpa_dense" in names
+    assert get_backend("ours").computes_moba and not get_backend("sdpa_dense").computes_moba
     cfg = MoBAConfig(block_size=128, top_k=8)
     for b in implementations.all_backends():
         assert isinstance(b, Backend)

@@ -220,3 +220,34 @@ def test_packed_backward_equals_each_sequence_alone(device):
         assert torch.equal(qq.grad[:, lo:lo + ln], a[0].grad), f"dq, sequence {r}"
         for ours, alone in zip((kk.grad, vv.grad), a[1:]):
             assert max_abs_error(ours[:, lo:lo + ln], alone.grad) < 2e-2, f"sequence {r}"
+
+
+@pytest.mark.parametrize("shape,h_kv", [((1, 1024, 4, 64), 4), ((2, 512, 8, 128), 2)])
+def test_every_block_selected_matches_dense_sdpa(device, shape, h_kv):
+    """top_k >= blocks: MoBA is dense causal attention, so the HIP forward
+    must agree with torch's fused SDPA (the `sdpa_dense` baseline backend)
+    within the bf16 bars -- a cross-check independent of the oracle."""
+    from implementations import get_backend
+
+    q, k, v = make_qkv(shape, torch.bfloat16, seed=11)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    cfg = MoBAConfig(block_size=128, top_k=shape[1] // 128)
+    qg, kg, vg = (t.to(device) for t in (q, k, v))
+    ours = moba_forward(qg, kg, vg, cfg).float()
+    dense = get_backend("sdpa_dense").forward(qg, kg, vg, cfg).float()
+    assert max_abs_error(ours, dense) <= BF16_MAX_ABS
+    assert mean_abs_error(ours, dense) <= BF16_MEAN_ABS
+
+
+def test_sdpa_dense_packed_equals_each_sequence_alone(device):
+    from implementations import get_backend
+
+    be = get_backend("sdpa_dense")
+    lens = [384, 128, 640]
+    cu = torch.tensor([0, 384, 512, 1152], dtype=torch.int32, device=device)
+    q, k, v = (t.to(device) for t in make_qkv((1, sum(lens), 4, 64), torch.bfloat16, seed=2))
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    packed = be.forward_packed(q, k, v, cfg, cu)
+    for lo, hi in zip(cu.tolist()[:-1], cu.tolist()[1:]):
+        alone = be.forward(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], cfg)
+        assert torch.equal(packed[:, lo:hi], alone)

@@ -215,3 +215,23 @@ def test_gate_rows_equal_the_full_gate_restricted(s, bs, tk):
     full = O.gate_select(q, kbar, c)
     rows = torch.tensor(sorted({0, 1, bs - 1, bs, 3 * bs + 7, s // 2, s - 2, s - 1}))
     assert torch.equal(O.gate_select_rows(q, kbar, c, rows), full[:, :, rows])
+
+
+@pytest.mark.parametrize("s,bs,tk", [(1000, 64, 4), (1024, 128, 8), (777, 32, 3), (256, 128, 8)])
+def test_sparsity_ratio_counts_the_selected_keys(s, bs, tk):
+    """The closed form behind the attainment ceiling equals the attended-key
+    count of real selections (the oracle gate on random inputs): own block's
+    causal prefix plus every key of each selected past block, over all
+    causally legal keys (reference `tests/test_bench.py` cross-check)."""
+    from moba.config import MoBAConfig
+    from moba.sparsity import sparsity_ratio
+
+    q, k, _ = qkv(1, s, 2, 32, dtype=torch.float32, seed=5)
+    sel = O.moba_selection(q, k, cfg(bs, tk))                    # [1, H, S, nb]
+    i = torch.arange(s)
+    key_block = torch.arange(s) // bs
+    visible = sel[..., key_block] & (torch.arange(s).view(1, -1) <= i.view(-1, 1))
+    attended = visible.sum(dtype=torch.float64) / sel.shape[1]
+    want = attended / (i + 1).sum(dtype=torch.float64)
+    got = sparsity_ratio(s, MoBAConfig(block_size=bs, top_k=tk))
+    assert abs(got - want.item()) < 1e-12
