@@ -1,21 +1,45 @@
 """MoBA attention as one differentiable operation
 (reference `src/moba/kernels/attention.py`).
 
-Saved for backward: q, k, v, out, lse (log2 units) and part_m (the
-written-marker of the per-slot partials); the CSC index rides on ctx. The
-gate receives no gradient (`attention.py:33-38`): routing is a hard top-k.
+Saved for backward: q, k, v, out and, per chunk, lse (log2 units), part_m
+(the written-marker of the per-slot partials) and the CSC index. The gate
+receives no gradient (`attention.py:33-38`): routing is a hard top-k.
 """
 
 import torch
 
+from moba import _lib
+from moba.chunking import partials_budget, plan_chunks, unit_bytes
 from moba.config import MoBAConfig
 from moba.kernels.moba_bwd import moba_backward
 from moba.kernels.moba_fwd import _validate, attend_partials, combine_partials
 from moba.kernels.routing import CSCIndex, build_csc_fused
 
 
+def _piece(t, b0, b1, h0, h1):
+    """t[b0:b1, :, h0:h1] as a contiguous tensor (a view when it already is)."""
+    return t[b0:b1, :, h0:h1].contiguous()
+
+
+def forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen):
+    """The chunks (b0, b1, hk0, hk1) of (batch row, kv head) units the
+    per-slot buffers of this call are split into (one chunk when they fit
+    the budget of `moba.chunking`)."""
+    _lib.require_gpu(q, k, v)  # raises before any device query on host tensors
+    b, s, h_q, d = q.shape
+    h_kv = k.shape[2]
+    rps = max_seqlen if cu_seqlens is not None else s
+    unit = unit_bytes(rps, h_q // h_kv, d, cfg.slots(), q.element_size())
+    return plan_chunks(b, h_kv, unit, partials_budget(q.device))
+
+
 class MoBAAttentionFunction(torch.autograd.Function):
-    """Differentiable MoBA attention over the HIP kernels (`attention.py:53-92`)."""
+    """Differentiable MoBA attention over the HIP kernels (`attention.py:53-92`).
+
+    Without a caller's index, a call whose per-slot buffers exceed the
+    budget of `moba.chunking` runs chunk by chunk over (batch row, kv head)
+    units, forward and backward, with the same results.
+    """
 
     @staticmethod
     def forward(ctx, q, k, v, cfg, index, causal, cu_seqlens, max_seqlen):
@@ -23,19 +47,50 @@ class MoBAAttentionFunction(torch.autograd.Function):
             cu_seqlens, max_seqlen = index.cu_seqlens, index.max_seqlen
         _validate(q, k, v, cfg, cu_seqlens, max_seqlen)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        if index is None:
-            index = build_csc_fused(q, k, cfg, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
-        part_m, part_l, part_acc = attend_partials(q, k, v, cfg, index, causal=causal)
-        out, lse = combine_partials(part_m, part_l, part_acc, q.dtype, return_lse=True)
-        ctx.save_for_backward(q, k, v, out, lse, part_m)
-        ctx.cfg, ctx.index, ctx.causal = cfg, index, causal
+        chunks = [(0, q.shape[0], 0, k.shape[2])] if index is not None else \
+            forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen)
+        group = q.shape[2] // k.shape[2]
+        out = torch.empty_like(q) if len(chunks) > 1 else None
+        saved = []
+        for b0, b1, hk0, hk1 in chunks:
+            whole = len(chunks) == 1
+            qc = q if whole else _piece(q, b0, b1, hk0 * group, hk1 * group)
+            kc = k if whole else _piece(k, b0, b1, hk0, hk1)
+            vc = v if whole else _piece(v, b0, b1, hk0, hk1)
+            idx = index if index is not None else build_csc_fused(
+                qc, kc, cfg, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+            part_m, part_l, part_acc = attend_partials(qc, kc, vc, cfg, idx, causal=causal)
+            oc, lse = combine_partials(part_m, part_l, part_acc, q.dtype, return_lse=True)
+            del part_l, part_acc
+            if whole:
+                out = oc
+            else:
+                out[b0:b1, :, hk0 * group:hk1 * group] = oc
+            saved.append((idx, lse, part_m))
+        ctx.save_for_backward(q, k, v, out)
+        ctx.cfg, ctx.causal, ctx.chunks, ctx.saved = cfg, causal, chunks, saved
+        ctx.index = saved[0][0] if len(chunks) == 1 else None
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out, lse, part_m = ctx.saved_tensors
-        dq, dk, dv = moba_backward(dout, q, k, v, out, lse, part_m, ctx.cfg, ctx.index,
-                                   causal=ctx.causal)
+        q, k, v, out = ctx.saved_tensors
+        chunks, group = ctx.chunks, q.shape[2] // k.shape[2]
+        if len(chunks) == 1:
+            idx, lse, part_m = ctx.saved[0]
+            dq, dk, dv = moba_backward(dout, q, k, v, out, lse, part_m, ctx.cfg, idx,
+                                       causal=ctx.causal)
+            return dq, dk, dv, None, None, None, None, None
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        for (b0, b1, hk0, hk1), (idx, lse, part_m) in zip(chunks, ctx.saved):
+            hq0, hq1 = hk0 * group, hk1 * group
+            g = moba_backward(_piece(dout, b0, b1, hq0, hq1), _piece(q, b0, b1, hq0, hq1),
+                              _piece(k, b0, b1, hk0, hk1), _piece(v, b0, b1, hk0, hk1),
+                              _piece(out, b0, b1, hq0, hq1), lse, part_m, ctx.cfg, idx,
+                              causal=ctx.causal)
+            dq[b0:b1, :, hq0:hq1] = g[0]
+            dk[b0:b1, :, hk0:hk1] = g[1]
+            dv[b0:b1, :, hk0:hk1] = g[2]
         return dq, dk, dv, None, None, None, None, None
 
 

@@ -165,8 +165,26 @@ def moba_forward(q, k, v, cfg: MoBAConfig, index: CSCIndex | None = None,
         cu_seqlens, max_seqlen = index.cu_seqlens, index.max_seqlen
     _validate(q, k, v, cfg, cu_seqlens, max_seqlen)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    if index is None:
-        index = build_csc_fused(q, k, cfg, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
-    part_m, part_l, part_acc = attend_partials(q, k, v, cfg, index, causal=causal,
-                                               partials_dtype=partials_dtype)
-    return combine_partials(part_m, part_l, part_acc, q.dtype)
+    if index is not None:
+        part_m, part_l, part_acc = attend_partials(q, k, v, cfg, index, causal=causal,
+                                                   partials_dtype=partials_dtype)
+        return combine_partials(part_m, part_l, part_acc, q.dtype)
+    # Without a caller's index the per-slot buffers are bounded by running
+    # (batch row, kv head) chunks (moba.chunking).
+    from moba.kernels.attention import _piece, forward_chunks
+    chunks = forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen)
+    group = q.shape[2] // k.shape[2]
+    out = torch.empty_like(q) if len(chunks) > 1 else None
+    for b0, b1, hk0, hk1 in chunks:
+        whole = len(chunks) == 1
+        qc = q if whole else _piece(q, b0, b1, hk0 * group, hk1 * group)
+        kc = k if whole else _piece(k, b0, b1, hk0, hk1)
+        vc = v if whole else _piece(v, b0, b1, hk0, hk1)
+        idx = build_csc_fused(qc, kc, cfg, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+        part_m, part_l, part_acc = attend_partials(qc, kc, vc, cfg, idx, causal=causal,
+                                                   partials_dtype=partials_dtype)
+        oc = combine_partials(part_m, part_l, part_acc, q.dtype)
+        if whole:
+            return oc
+        out[b0:b1, :, hk0 * group:hk1 * group] = oc
+    return out

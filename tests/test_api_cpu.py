@@ -126,3 +126,22 @@ def test_index_stride_layouts():
         index_stride(make(*wide))                      # padding between kv heads
     even = [t[:, :, ::2] for t in sep]                 # uniform stride 2 is fine
     assert index_stride(make(*even)) == 2
+
+
+@pytest.mark.parametrize("batch,h_kv,budget_units", [(1, 4, 100), (2, 4, 8), (3, 4, 4), (2, 4, 3),
+                                                     (2, 8, 1), (1, 1, 0)])
+def test_partials_chunk_plan(batch, h_kv, budget_units):
+    """Every (batch row, kv head) unit lands in exactly one chunk, chunks
+    stay within the budget unless one unit alone exceeds it, and a budget
+    that holds everything gives a single chunk."""
+    from moba.chunking import plan_chunks
+
+    unit = 1000
+    chunks = plan_chunks(batch, h_kv, unit, budget_units * unit)
+    seen = [(b, h) for b0, b1, h0, h1 in chunks for b in range(b0, b1) for h in range(h0, h1)]
+    assert sorted(seen) == [(b, h) for b in range(batch) for h in range(h_kv)]
+    for b0, b1, h0, h1 in chunks:
+        assert (b1 - b0) * (h1 - h0) * unit <= max(unit, budget_units * unit)
+        assert b1 - b0 == 1 or (h0, h1) == (0, h_kv)   # rectangles: whole rows or one row
+    if budget_units >= batch * h_kv:
+        assert chunks == [(0, batch, 0, h_kv)]

@@ -251,3 +251,51 @@ def test_sdpa_dense_packed_equals_each_sequence_alone(device):
     for lo, hi in zip(cu.tolist()[:-1], cu.tolist()[1:]):
         alone = be.forward(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], cfg)
         assert torch.equal(packed[:, lo:hi], alone)
+
+
+@pytest.mark.parametrize("shape,h_kv,units", [((2, 1024, 8, 64), 2, 1), ((3, 768, 4, 64), 4, 4),
+                                              ((1, 1024, 8, 128), 4, 2)])
+def test_chunked_partials_equal_one_pass(device, monkeypatch, shape, h_kv, units):
+    """Per-slot buffers bounded to `units` (batch row, kv head) units: the
+    forward is bitwise the unchunked one (every stage works per row and kv
+    head), the gradients agree within the bf16 bars (dK / dV sum a column's
+    entries in an order the atomic CSC build does not fix)."""
+    from moba.chunking import ENV_BUDGET, unit_bytes
+
+    q, k, v, do = make_qkv(shape, torch.bfloat16, seed=4, n=4)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    cfg = MoBAConfig(block_size=128, top_k=4)
+    qg, kg, vg, dog = (t.to(device) for t in (q, k, v, do))
+
+    def run():
+        fwd = moba_forward(qg, kg, vg, cfg)
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (qg, kg, vg))
+        out = moba_attention(qq, kk, vv, cfg)
+        out.backward(dog)
+        return fwd, out.detach(), qq.grad, kk.grad, vv.grad
+
+    monkeypatch.setenv(ENV_BUDGET, str(1 << 40))
+    whole = run()
+    unit = unit_bytes(shape[1], shape[2] // h_kv, shape[3], cfg.slots(), 2)
+    monkeypatch.setenv(ENV_BUDGET, str(units * unit))
+    chunked = run()
+    assert torch.equal(whole[0], chunked[0]) and torch.equal(whole[1], chunked[1])
+    assert torch.equal(whole[0], whole[1])
+    for a, b in zip(whole[2:], chunked[2:]):
+        assert max_abs_error(a.float(), b.float()) <= BF16_MAX_ABS
+        assert mean_abs_error(a.float(), b.float()) <= BF16_MEAN_ABS
+
+
+def test_chunked_partials_packed(device, monkeypatch):
+    """Packed sequences chunk over kv heads; same output as one pass."""
+    from moba.chunking import ENV_BUDGET
+
+    lens = [640, 384, 1024]
+    cu = torch.tensor([0, 640, 1024, 2048], dtype=torch.int32, device=device)
+    q, k, v = (t.to(device) for t in make_qkv((1, sum(lens), 4, 64), torch.bfloat16, seed=6))
+    cfg = MoBAConfig(block_size=128, top_k=4)
+    monkeypatch.setenv(ENV_BUDGET, str(1 << 40))
+    whole = moba_forward(q, k, v, cfg, cu_seqlens=cu, max_seqlen=1024)
+    monkeypatch.setenv(ENV_BUDGET, "1")
+    chunked = moba_forward(q, k, v, cfg, cu_seqlens=cu, max_seqlen=1024)
+    assert torch.equal(whole, chunked)
