@@ -95,6 +95,10 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * an atomic cursor, so their order inside a column is unspecified (as in the
  * reference, routing.py:35-52); each (query, slot) pair appears exactly
  * once. row_indices hold packed token indices when cu_seqlens is given.
+ * Ids outside [0, n_blocks), and ids past the last block a query of the
+ * same 1024-query tile can see, are ignored like the -1 padding (moba_gate
+ * never writes them; the guard keeps a bad caller buffer from addressing
+ * memory).
  * Entry i of the three index arrays is element i * index_stride of each:
  * index_stride 1 for three separate arrays, 3 for one array of (row, head,
  * slot) records passed as base, base + 1, base + 2 (one record per entry

@@ -45,7 +45,7 @@ count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __
   const int64_t tok = sp.bos + t;
   const int64_t qid = packed ? hq * S + tok : (r * h_q + hq) * S + t;
   const int32_t blk = block_idx[qid * slots + j];
-  if (blk < 0) return;
+  if (blk < 0 || blk >= n_blocks) return;  // padding, or an id no query can hold
   const int64_t colbase = (r * h_kv + hk) * n_blocks;
   const int32_t within = atomicAdd(&col_nnz_or_cursor[colbase + blk], 1);
   if (kScatter) {
@@ -129,7 +129,7 @@ tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
     const bool live = query(i, t, tok, qid);
     for (int j = 0; j < slots; ++j) {
       const int32_t blk = live ? block_idx[qid * slots + j] : -1;
-      bin_add(bins, blk, blk >= 0);
+      bin_add(bins, blk, blk >= 0 && blk < nvis);
     }
   }
   __syncthreads();
@@ -151,8 +151,9 @@ tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
     const bool live = query(i, t, tok, qid);
     for (int j = 0; j < slots; ++j) {
       const int32_t blk = live ? block_idx[qid * slots + j] : -1;
-      const int32_t pos = bin_add(bins, blk, blk >= 0);
-      if (blk < 0) continue;
+      const bool ok = blk >= 0 && blk < nvis;
+      const int32_t pos = bin_add(bins, blk, ok);
+      if (!ok) continue;
       const int64_t dst = (ibase + pos) * istride;
       const int32_t rv = static_cast<int32_t>(packed ? tok : t);
       if (records) {  // (row, head, slot) adjacent: one 12-byte store

@@ -86,3 +86,30 @@ def test_csc_unselected_columns_exist(device):
     index = build_csc_fused(q, k, cfg)
     assert bool((index.col_nnz == 0).any())
     assert int(index.col_offsets[0, 0, -1]) == int(index.col_nnz[0, 0].sum())
+
+
+def test_csc_ignores_ids_no_query_can_hold(device):
+    """Ids outside [0, n_blocks) -- one past the end, or negative other than
+    the -1 padding -- never reach an address: the build ignores them, as if
+    they were padding. (The gate never writes them; the guard is for caller
+    buffers passed through the C ABI.)"""
+    from moba.kernels.gating import gate_select
+    from moba.kernels.pooling import pool_blocks
+
+    cfg = MoBAConfig(block_size=64, top_k=4)
+    q, k, _ = make_qkv((1, 1024, 2, 64), torch.bfloat16, seed=7, device=device)
+    nb = 1024 // 64
+    idx = gate_select(q, pool_blocks(k, cfg), cfg)
+    g = torch.Generator().manual_seed(3)
+    pick = torch.rand(idx.shape, generator=g) < 0.1
+    bad = idx.clone()
+    bad[pick.to(device) & (torch.arange(4, device=device) % 2 == 0)] = nb
+    bad[pick.to(device) & (torch.arange(4, device=device) % 2 == 1)] = -7
+    want = build_csc_from_indices(torch.where(pick.to(device), -1, idx), nb, cfg)
+    got = build_csc_from_indices(bad, nb, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(got.col_nnz, want.col_nnz)
+    assert torch.equal(got.col_offsets, want.col_offsets)
+    for blk in range(nb):
+        assert column_sets(got, 0, 0, blk) == column_sets(want, 0, 0, blk)
+        assert column_sets(got, 0, 1, blk) == column_sets(want, 0, 1, blk)
