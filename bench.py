@@ -99,7 +99,7 @@ def stage_times(s, dev, reps=5):
     """Per-stage device time (ms) of one fwd+bwd, each stage timed alone."""
     from moba.config import MoBAConfig
     from moba.kernels.gating import gate_select
-    from moba.kernels.moba_bwd import compute_delta, reduce_dq
+    from moba.kernels.moba_bwd import bwd_kernel, compute_delta, reduce_dq
     from moba.kernels.moba_fwd import attend_partials, combine_partials
     from moba.kernels.pooling import pool_blocks
     from moba.kernels.routing import build_csc_from_indices
@@ -127,13 +127,7 @@ def stage_times(s, dev, reps=5):
     dq_part = torch.empty((1, HEADS, s, TOPK, HEAD_DIM), device=dev, dtype=q.dtype)
 
     def bwd():
-        _lib.call("moba_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(do),
-                  _lib.ptr(lse_delta), _lib.ptr(index.col_nnz),
-                  _lib.ptr(index.col_offsets), _lib.ptr(index.row_indices),
-                  _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
-                  _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),
-                  None, 1, s, s, HEADS, HEADS, HEAD_DIM, index.num_blocks, BLOCK, TOPK,
-                  index.row_indices.shape[-1], 3, 1, 0, 0, _lib.stream_handle(dev))
+        bwd_kernel(do, q, k, v, lse_delta, cfg, index, dk, dv, dq_part)
 
     st["bwd"] = timed(bwd, reps, 1)[0]
     st["dq_reduce"] = timed(lambda: reduce_dq(dq_part, parts[0], q.dtype), reps, 1)[0]

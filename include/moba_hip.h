@@ -47,9 +47,10 @@ enum moba_status {
 
 enum moba_dtype { MOBA_BF16 = 0, MOBA_FP16 = 1, MOBA_FP32 = 2 };
 
-/* Library identity. moba_abi_version() is 3: (m, l) and (lse, delta) travel
- * as 8-byte pairs, and the CSC index arrays take an element stride (version
- * 1 took separate statistics arrays; version 2 had no index stride). */
+/* Library identity. moba_abi_version() is 4: (m, l) and (lse, delta) travel
+ * as 8-byte pairs, the CSC index arrays take an element stride, and the CSC
+ * build can emit a segment list that attend and backward take (version 1
+ * took separate statistics arrays; 2 had no index stride; 3 no segments). */
 int moba_abi_version(void);
 const char* moba_last_error(void);
 const char* moba_status_string(int status);
@@ -103,6 +104,14 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * index_stride 1 for three separate arrays, 3 for one array of (row, head,
  * slot) records passed as base, base + 1, base + 2 (one record per entry
  * keeps each scattered entry in one memory sector).
+ * Segment list (optional; segments == NULL skips it): each (row, kv head)'s
+ * columns in `order`, a column of n entries cut into min(max_seg,
+ * ceil(n / seg_len)) segments of near-equal length, so one long column is
+ * worked on by several programs. segments [R, Hkv, seg_cap, 4] int32 holds
+ * (block, segment, segments of the column, scratch slot or -1); seg_split
+ * [R, Hkv, seg_cap - nb] the first segment of every cut column; seg_counts
+ * [R, Hkv, 2] the numbers of segments and of cut columns. seg_cap must be at
+ * least nb + ceil((Hq/Hkv) * rows_per_seq * slots / seg_len).
  * Replaces build_csc_from_indices (src/moba/kernels/routing.py:309-427)
  * and its three kernels (routing.py:139-301); CSCIndex fields of
  * routing.py:73-130.
@@ -116,7 +125,9 @@ int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                    int32_t* order, const int32_t* cu_seqlens, int64_t batch,
                    int64_t seq_len, int64_t max_seqlen, int64_t h_q,
                    int64_t h_kv, int64_t n_blocks, int64_t slots,
-                   int64_t index_stride, void* workspace, size_t workspace_bytes,
+                   int64_t index_stride, int32_t* segments, int32_t* seg_split,
+                   int32_t* seg_counts, int64_t seg_cap, int64_t seg_len,
+                   int64_t max_seg, void* workspace, size_t workspace_bytes,
                    void* stream);
 
 /*
@@ -127,7 +138,8 @@ int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
  * one 8-byte pair: part_ml [B, Hq, S, slots, 2] fp32 = (m, l); part_acc
  * [B, Hq, S, slots, D]. Unwritten slots keep m = -inf, which this call sets
  * before the kernel runs. The index arrays and index_stride are those of
- * moba_csc_build.
+ * moba_csc_build; with its segment list (segments != NULL) each segment is
+ * one program, else each column.
  * Replaces attend_partials (src/moba/kernels/moba_fwd.py:566-665) and
  * moba_fwd_kernel (moba_fwd.py:230-425).
  */
@@ -140,6 +152,8 @@ int moba_attend(const void* q, const void* k, const void* v,
                 int64_t max_seqlen, int64_t h_q, int64_t h_kv,
                 int64_t head_dim, int64_t n_blocks, int64_t block_size,
                 int64_t slots, int64_t index_cap, int64_t index_stride,
+                const int32_t* segments, const int32_t* seg_split,
+                const int32_t* seg_counts, int64_t seg_cap,
                 int causal, int dtype, int acc_dtype, void* stream);
 
 /*
@@ -173,7 +187,10 @@ int moba_bwd_delta(const void* out, const void* dout, const float* lse,
  * moba_backward (src/moba/kernels/moba_bwd.py:506-579; kernel
  * moba_bwd.py:216-394). lse_delta: the (lse, delta) pairs moba_bwd_delta
  * writes, lse in log2 units as moba_combine writes it. The index arrays and
- * index_stride are those of moba_csc_build.
+ * index_stride are those of moba_csc_build. With its segment list, the
+ * segments of a cut column leave float32 dK / dV sums in seg_scratch
+ * ([R, Hkv, scratch_cap, 2, bs, D] float32, scratch_cap >= 2 * (seg_cap -
+ * nb)), which this call then adds in segment order into dK / dV.
  */
 int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
              const float* lse_delta, const int32_t* col_nnz,
@@ -183,7 +200,9 @@ int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
              const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
              int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
              int64_t n_blocks, int64_t block_size, int64_t slots,
-             int64_t index_cap, int64_t index_stride, int causal, int dtype,
+             int64_t index_cap, int64_t index_stride, const int32_t* segments,
+             const int32_t* seg_split, const int32_t* seg_counts, int64_t seg_cap,
+             float* seg_scratch, int64_t scratch_cap, int causal, int dtype,
              int acc_dtype, void* stream);
 
 /*

@@ -29,26 +29,55 @@ struct AttnArgs {
   int causal;
   float scale_log2;       // D^-1/2 * log2(e)
   float scale;            // D^-1/2
+  // Segment list (4 ints per entry: block, segment, segments of the column,
+  // scratch slot) or null for one workgroup per whole column.
+  const int32_t* seg;
+  const int32_t* seg_split;   // first segment of every cut column
+  const int32_t* seg_counts;  // per (row, kv head): segments, cut columns
+  int64_t seg_cap;            // entries per (row, kv head)
+  float* seg_scratch;         // backward: fp32 dK / dV of cut columns' segments
+  int64_t scratch_cap;        // scratch slots per (row, kv head)
 };
 
 // Per-column context resolved from (program column position, row * h_kv).
 struct Column {
   int64_t r, hk;
   int64_t blk;
-  int32_t n;       // entries in the column
+  int32_t n;       // entries in the column (segment)
+  int32_t nseg;    // segments the column is cut into (1: whole)
+  int32_t scratch; // scratch slot of this segment when nseg > 1
+  bool skip;       // a program past the segment list: nothing to do
   int64_t lo;      // offset of the column in the index arrays (incl. row base)
   int64_t key0;    // first key position, in the frame row_indices use
   int64_t key_end; // one past the last valid key position, same frame
   int64_t tok0;    // global token index of key0 (addresses K / V)
 };
 
-__device__ inline Column resolve_column(const AttnArgs& a, int64_t col_pos, int64_t rh) {
+__device__ inline Column resolve_column(const AttnArgs& a, int64_t x, int64_t rh) {
+  // One return path, every field computed on both: an early return here
+  // leaves the struct in scratch memory, read back inside the kernels' loops.
   Column c;
   c.r = rh / a.h_kv;
   c.hk = rh % a.h_kv;
-  c.blk = a.order[rh * a.n_blocks + col_pos];
-  c.n = a.col_nnz[rh * a.n_blocks + c.blk];
-  c.lo = rh * a.cap + a.col_offsets[rh * (a.n_blocks + 1) + c.blk];
+  int64_t s = 0;
+  c.nseg = 1;
+  c.scratch = -1;
+  c.skip = false;
+  if (a.seg) {
+    // Past the list: entry 0 (every column has one) with nothing to do.
+    c.skip = x >= a.seg_counts[2 * rh];
+    const int32_t* e = a.seg + (rh * a.seg_cap + (c.skip ? 0 : x)) * 4;
+    c.blk = e[0];
+    s = e[1];
+    c.nseg = e[2];
+    c.scratch = e[3];
+  } else {
+    c.blk = a.order[rh * a.n_blocks + x];
+  }
+  const int64_t n_all = a.col_nnz[rh * a.n_blocks + c.blk];
+  const int64_t e0 = n_all * s / c.nseg, e1 = n_all * (s + 1) / c.nseg;
+  c.n = c.skip ? 0 : static_cast<int32_t>(e1 - e0);
+  c.lo = rh * a.cap + a.col_offsets[rh * (a.n_blocks + 1) + c.blk] + e0;
   if (a.cu) {
     const int64_t bos = a.cu[c.r], eos = a.cu[c.r + 1];
     c.key0 = bos + c.blk * a.bs;                     // packed: global tokens

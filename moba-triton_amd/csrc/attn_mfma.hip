@@ -329,7 +329,7 @@ attend_mfma_kernel(AttnArgs a) {
 
 template <typename T, typename A, int D, int BS>
 static int launch_attend(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
-  dim3 grid(static_cast<unsigned>(a.n_blocks), static_cast<unsigned>(n_cols));
+  dim3 grid(static_cast<unsigned>(a.seg ? a.seg_cap : a.n_blocks), static_cast<unsigned>(n_cols));
   hipLaunchKernelGGL((attend_mfma_kernel<T, A, D, BS>), grid, dim3(256), 0, st, a);
   return check_launch("moba_attend (mfma)");
 }
@@ -409,6 +409,7 @@ bwd_mfma_kernel(AttnArgs a) {
   __shared__ int64_t s_dst[NQ];
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
+  if (c.skip) return;  // past the segment list (uniform)
   const int tid = threadIdx.x;
   const uint16_t* Kg = static_cast<const uint16_t*>(a.k);
   const uint16_t* Vg = static_cast<const uint16_t*>(a.v);
@@ -678,6 +679,28 @@ bwd_mfma_kernel(AttnArgs a) {
   }
 
   // dK, dV of this lane's key: register v is feature 32dt + 8(v/4) + 4h + v%4.
+  // A segment of a cut column leaves its float32 sums in its scratch slot
+  // ([2][BS][D]: dK scaled, dV); the finishing pass adds the column's
+  // segments in order.
+  if (c.nseg > 1) {
+    if (mykey < key_lim) {
+      float* sk = a.seg_scratch +
+                  (static_cast<int64_t>(blockIdx.y) * a.scratch_cap + c.scratch) * 2 * BS * D +
+                  mykey * D + 4 * h;
+      float* sv = sk + BS * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          store4<float>(sk + dt * 32 + 8 * q4, dk[dt][4 * q4] * a.scale,
+                        dk[dt][4 * q4 + 1] * a.scale, dk[dt][4 * q4 + 2] * a.scale,
+                        dk[dt][4 * q4 + 3] * a.scale);
+          store4<float>(sv + dt * 32 + 8 * q4, dv[dt][4 * q4], dv[dt][4 * q4 + 1],
+                        dv[dt][4 * q4 + 2], dv[dt][4 * q4 + 3]);
+        }
+    }
+    return;
+  }
   if (mykey < key_lim) {
     const int64_t off = ((c.tok0 + mykey) * a.h_kv + c.hk) * D + 4 * h;
     T* dK = static_cast<T*>(a.dk) + off;
@@ -697,7 +720,7 @@ bwd_mfma_kernel(AttnArgs a) {
 template <typename T, typename A, int D, int BS>
 static int launch_bwd(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
   constexpr int NQ = D == 128 ? 32 : 64;
-  dim3 grid(static_cast<unsigned>(a.n_blocks), static_cast<unsigned>(n_cols));
+  dim3 grid(static_cast<unsigned>(a.seg ? a.seg_cap : a.n_blocks), static_cast<unsigned>(n_cols));
   hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS, NQ>), grid, dim3(BS * 2), 0, st, a);
   return check_launch("moba_bwd (mfma)");
 }

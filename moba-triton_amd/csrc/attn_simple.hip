@@ -484,6 +484,44 @@ dq_reduce_kernel(const A* __restrict__ dq_part, const float* __restrict__ part_m
   store8<O>(dq + ((b * S + t) * h_q + h) * D + d0, acc);
 }
 
+// dK / dV of the cut columns: the column's segments' float32 sums (scratch
+// slots x .. x + nseg - 1, [2][BS][D] each) added in segment order, written
+// in the input dtype. One workgroup per cut column of a (row, kv head).
+template <typename T>
+__global__ void __launch_bounds__(256)
+seg_finish_kernel(AttnArgs a) {
+  const int64_t rh = blockIdx.y;
+  const int64_t extra_cap = a.seg_cap - a.n_blocks;
+  if (static_cast<int64_t>(blockIdx.x) >= a.seg_counts[2 * rh + 1]) return;
+  const int32_t first = a.seg_split[rh * extra_cap + blockIdx.x];
+  const Column c = resolve_column(a, first, rh);
+  const int64_t bsd = a.bs * a.D;
+  const float* base = a.seg_scratch + (rh * a.scratch_cap + c.scratch) * 2 * bsd;
+  const int key_lim = static_cast<int>(c.key_end - c.key0);
+  T* dK = static_cast<T*>(a.dk);
+  T* dV = static_cast<T*>(a.dv);
+  // Thread -> (key, four features): D / 4 threads per key row (the MFMA
+  // backward, the only producer of segments, has D of 64 or 128).
+  const int v4 = static_cast<int>(a.D / 4);
+  const int per = static_cast<int>(blockDim.x) / v4;
+  const int c4 = static_cast<int>(threadIdx.x) % v4;
+  for (int key = static_cast<int>(threadIdx.x) / v4; key < key_lim; key += per) {
+    const int64_t i = static_cast<int64_t>(key) * a.D + 4 * c4;
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+    for (int j = 0; j < c.nseg; ++j) {
+      const float4 x = *reinterpret_cast<const float4*>(base + j * 2 * bsd + i);
+      const float4 y = *reinterpret_cast<const float4*>(base + j * 2 * bsd + bsd + i);
+      sk.x += x.x; sk.y += x.y; sk.z += x.z; sk.w += x.w;
+      sv.x += y.x; sv.y += y.y; sv.z += y.z; sv.w += y.w;
+    }
+    const int64_t off = ((c.tok0 + key) * a.h_kv + c.hk) * a.D + 4 * c4;
+    Elem<T>::store(dK, off, sk.x); Elem<T>::store(dK, off + 1, sk.y);
+    Elem<T>::store(dK, off + 2, sk.z); Elem<T>::store(dK, off + 3, sk.w);
+    Elem<T>::store(dV, off, sv.x); Elem<T>::store(dV, off + 1, sv.y);
+    Elem<T>::store(dV, off + 2, sv.z); Elem<T>::store(dV, off + 3, sv.w);
+  }
+}
+
 __global__ void __launch_bounds__(256)
 fill_f32_kernel(float* __restrict__ p, int64_t n, float value) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -527,6 +565,19 @@ static int prepare_attn(AttnArgs* a, Geometry* g, const void* q, const void* k,
   return MOBA_OK;
 }
 
+// Segment list of moba_csc_build (null: one program per whole column).
+static int set_segments(AttnArgs* a, const int32_t* segments, const int32_t* seg_split,
+                        const int32_t* seg_counts, int64_t seg_cap) {
+  if (!segments) return MOBA_OK;
+  if (!seg_split || !seg_counts || seg_cap < a->n_blocks)
+    return fail(MOBA_ERR_INVALID, "segment list: need split / counts and seg_cap >= n_blocks");
+  a->seg = segments;
+  a->seg_split = seg_split;
+  a->seg_counts = seg_counts;
+  a->seg_cap = seg_cap;
+  return MOBA_OK;
+}
+
 static bool simple_shape_ok(const Geometry& g) {
   return g.head_dim <= 128 && g.head_dim >= 8 && g.block_size * g.head_dim <= 16384;
 }
@@ -563,6 +614,8 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
                            int64_t max_seqlen, int64_t h_q, int64_t h_kv,
                            int64_t head_dim, int64_t n_blocks, int64_t block_size,
                            int64_t slots, int64_t index_cap, int64_t index_stride,
+                           const int32_t* segments, const int32_t* seg_split,
+                           const int32_t* seg_counts, int64_t seg_cap,
                            int causal, int dtype, int acc_dtype, void* stream) {
   using namespace moba;
   AttnArgs a;
@@ -574,6 +627,8 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
   if (st) return st;
   if (!part_ml || !part_acc) return fail(MOBA_ERR_INVALID, "null partials");
   a.part_ml = part_ml; a.part_acc = part_acc;
+  st = set_segments(&a, segments, seg_split, seg_counts, seg_cap);
+  if (st) return st;
   hipStream_t s = as_stream(stream);
   // Unwritten slots must read as m = -inf: the marker combine and dq reduce
   // rely on. The (m, l) pairs are cleared whole; l / acc of such slots are
@@ -585,6 +640,7 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
   if (st) return st;
   st = attend_mfma(a, dtype, acc_dtype, batch * h_kv, s);
   if (st != MOBA_ERR_UNSUPPORTED) return st;
+  a.seg = nullptr;  // the FMA kernels take whole columns
   if (!simple_shape_ok(g))
     return fail(MOBA_ERR_UNSUPPORTED, "attend: block_size * head_dim must be <= 16384");
   const size_t lds = sizeof(float) * (2 * block_size * head_dim + kE * head_dim +
@@ -666,7 +722,9 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
                         const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
                         int64_t max_seqlen, int64_t h_q, int64_t h_kv, int64_t head_dim,
                         int64_t n_blocks, int64_t block_size, int64_t slots,
-                        int64_t index_cap, int64_t index_stride, int causal, int dtype,
+                        int64_t index_cap, int64_t index_stride, const int32_t* segments,
+                        const int32_t* seg_split, const int32_t* seg_counts, int64_t seg_cap,
+                        float* seg_scratch, int64_t scratch_cap, int causal, int dtype,
                         int acc_dtype, void* stream) {
   using namespace moba;
   AttnArgs a;
@@ -679,9 +737,25 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
   if (!dout || !lse_delta || !dk || !dv || !dq_part)
     return fail(MOBA_ERR_INVALID, "null pointer");
   a.dout = dout; a.lse_delta = lse_delta; a.dk = dk; a.dv = dv; a.part_acc = dq_part;
+  st = set_segments(&a, segments, seg_split, seg_counts, seg_cap);
+  if (st) return st;
+  if (a.seg) {
+    if (!seg_scratch || scratch_cap < 2 * (seg_cap - n_blocks))
+      return fail(MOBA_ERR_INVALID, "segment scratch: need scratch_cap >= 2 * (seg_cap - n_blocks)");
+    a.seg_scratch = seg_scratch;
+    a.scratch_cap = scratch_cap;
+  }
   hipStream_t s = as_stream(stream);
   st = bwd_mfma(a, dtype, acc_dtype, batch * h_kv, s);
+  if (st == MOBA_OK && a.seg && seg_cap > n_blocks) {
+    dim3 fgrid(static_cast<unsigned>(seg_cap - n_blocks), static_cast<unsigned>(batch * h_kv));
+    st = MOBA_DISPATCH_DTYPE(dtype, T, [&] {
+      hipLaunchKernelGGL(seg_finish_kernel<T>, fgrid, dim3(256), 0, s, a);
+      return check_launch("moba_bwd (cut columns)");
+    });
+  }
   if (st != MOBA_ERR_UNSUPPORTED) return st;
+  a.seg = nullptr;  // the FMA kernels take whole columns
   if (head_dim > 128 || head_dim < 8)
     return fail(MOBA_ERR_UNSUPPORTED, "backward: head_dim must be in [8, 128]");
   const int64_t tiles = cdiv(block_size, kKT);

@@ -227,6 +227,79 @@ order_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ order,
   if (c < n_blocks && sub == 0) order[rh * n_blocks + rank] = static_cast<int32_t>(c);
 }
 
+// Segment list of one (row, kv head): its columns in `order` (longest first),
+// a column of n entries cut into min(max_seg, ceil(n / seg_len)) segments of
+// near-equal length (at least one, also when empty). Entry (c, s, nseg, x):
+// column (block id) c, segment s of nseg, and x = the segment's slot in the
+// dK / dV scratch when nseg > 1 (else -1). split[rh * (cap - n_blocks) + i]
+// lists the first segment of every cut column; counts[2 rh] / counts[2 rh + 1]
+// hold the numbers of segments and of cut columns. One workgroup per
+// (row, kv head); writes past the capacities are dropped (the caller sizes
+// them from an upper bound, so none happen).
+__global__ void __launch_bounds__(1024)
+seg_build_kernel(const int32_t* __restrict__ col_nnz, const int32_t* __restrict__ order,
+                 int64_t n_blocks, int64_t seg_len, int max_seg, int32_t* __restrict__ seg,
+                 int32_t* __restrict__ split, int32_t* __restrict__ counts, int64_t cap) {
+  __shared__ int32_t sa[1024], sb[1024];
+  const int64_t rh = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t extra_cap = cap - n_blocks;
+  // Inclusive scan of sa (and sb) over the workgroup.
+  auto scan = [&](bool both) {
+    for (int w = 1; w < 1024; w <<= 1) {
+      const int32_t x = tid >= w ? sa[tid - w] : 0;
+      const int32_t y = both && tid >= w ? sb[tid - w] : 0;
+      __syncthreads();
+      sa[tid] += x;
+      if (both) sb[tid] += y;
+      __syncthreads();
+    }
+  };
+  int32_t carry_seg = 0, carry_scr = 0, carry_split = 0;
+  for (int64_t base = 0; base < n_blocks; base += 1024) {
+    const int64_t p = base + tid;
+    int32_t nseg = 0;
+    if (p < n_blocks) {
+      const int64_t n = col_nnz[rh * n_blocks + order[rh * n_blocks + p]];
+      const int64_t k = (n + seg_len - 1) / seg_len;
+      nseg = static_cast<int32_t>(k < 1 ? 1 : (k > max_seg ? max_seg : k));
+    }
+    const int32_t nscr = nseg > 1 ? nseg : 0;
+    sa[tid] = nseg;
+    sb[tid] = nscr;
+    __syncthreads();
+    scan(true);
+    const int32_t first = carry_seg + sa[tid] - nseg;
+    const int32_t first_scr = carry_scr + sb[tid] - nscr;
+    const int32_t tot_seg = sa[1023], tot_scr = sb[1023];
+    for (int32_t j = 0; j < nseg; ++j) {
+      const int64_t at = first + j;
+      if (at < cap) {
+        int32_t* e = seg + (rh * cap + at) * 4;
+        e[0] = order[rh * n_blocks + p];
+        e[1] = j;
+        e[2] = nseg;
+        e[3] = nscr ? first_scr + j : -1;
+      }
+    }
+    __syncthreads();  // every thread has read the scans
+    sa[tid] = nscr ? 1 : 0;
+    __syncthreads();
+    scan(false);
+    if (nscr && carry_split + sa[tid] - 1 < extra_cap)
+      split[rh * extra_cap + carry_split + sa[tid] - 1] = first;
+    const int32_t tot_split = sa[1023];
+    __syncthreads();
+    carry_seg += tot_seg;
+    carry_scr += tot_scr;
+    carry_split += tot_split;
+  }
+  if (tid == 0) {
+    counts[2 * rh] = carry_seg < cap ? carry_seg : static_cast<int32_t>(cap);
+    counts[2 * rh + 1] = carry_split < extra_cap ? carry_split : static_cast<int32_t>(extra_cap);
+  }
+}
+
 }  // namespace moba
 
 extern "C" size_t moba_csc_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q,
@@ -241,8 +314,10 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                               int32_t* order, const int32_t* cu_seqlens, int64_t batch,
                               int64_t seq_len, int64_t max_seqlen, int64_t h_q,
                               int64_t h_kv, int64_t n_blocks, int64_t slots,
-                              int64_t index_stride, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+                              int64_t index_stride, int32_t* segments, int32_t* seg_split,
+                              int32_t* seg_counts, int64_t seg_cap, int64_t seg_len,
+                              int64_t max_seg, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   using namespace moba;
   Geometry g;
   const int64_t rps = cu_seqlens ? max_seqlen : seq_len;
@@ -251,6 +326,10 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   if (st) return st;
   if (slots <= 0) return fail(MOBA_ERR_INVALID, "slots must be positive");
   if (index_stride < 1) return fail(MOBA_ERR_INVALID, "index_stride must be positive");
+  if (segments && (!seg_split || !seg_counts || seg_cap < n_blocks || seg_len < 1 ||
+                   max_seg < 1 || max_seg > 64))
+    return fail(MOBA_ERR_INVALID, "segment list: need split / counts, seg_cap >= n_blocks, "
+                                  "seg_len >= 1, 1 <= max_seg <= 64");
   if (!block_idx || !col_nnz || !col_offsets || !row_indices || !head_indices ||
       !slot_of_pair || !order)
     return fail(MOBA_ERR_INVALID, "null pointer");
@@ -292,6 +371,10 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                      dim3(static_cast<unsigned>(cdiv(n_blocks, 32)),
                           static_cast<unsigned>(batch * h_kv)),
                      dim3(256), 0, s, col_nnz, order, n_blocks);
+  if (segments)
+    hipLaunchKernelGGL(seg_build_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024),
+                       0, s, col_nnz, order, n_blocks, seg_len, static_cast<int>(max_seg),
+                       segments, seg_split, seg_counts, seg_cap);
   if (tiled)
     hipLaunchKernelGGL(tile_count_or_scatter_kernel<true>, tgrid, dim3(kTileT), 0, s,
                        block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,

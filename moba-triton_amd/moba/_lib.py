@@ -36,13 +36,15 @@ SIGNATURES = {
                        _I, _I, _P, _Z, _P]),
     "moba_csc_workspace_size": (_Z, [_L, _L, _L, _L, _L, _L]),
     "moba_csc_build": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L,
-                            _L, _L, _L, _P, _Z, _P]),
+                            _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _Z, _P]),
     "moba_attend": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                         _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P]),
+                         _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L,
+                         _I, _I, _I, _P]),
     "moba_combine": (_I, [_P, _P, _P, _P, _L, _L, _L, _L, _L, _I, _I, _P]),
     "moba_bwd_delta": (_I, [_P, _P, _P, _P, _L, _L, _L, _L, _I, _P]),
     "moba_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                      _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _I, _I, _I, _P]),
+                      _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L, _P, _L,
+                      _I, _I, _I, _P]),
     "moba_dq_reduce": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _I, _P]),
 }
 

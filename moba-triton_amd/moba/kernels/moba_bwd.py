@@ -47,6 +47,35 @@ def reduce_dq(dq_part: torch.Tensor, part_m: torch.Tensor, out_dtype) -> torch.T
     return dq
 
 
+def bwd_kernel(dout, q, k, v, lse_delta, cfg: MoBAConfig, index: CSCIndex, dk, dv, dq_part,
+               causal: bool = True) -> None:
+    """The KV-block-major backward launch (`moba_bwd.py:216-394`): dK, dV
+    and one dQ partial per (query, slot), from contiguous q / k / v / dO on
+    the GPU and the (lse, delta) pairs of `compute_delta`."""
+    b, s, h_q, d = q.shape
+    h_kv = k.shape[2]
+    dev = q.device
+    rows = index.col_nnz.shape[0]
+    mx = index.max_seqlen if index.cu_seqlens is not None else s
+    # float32 dK / dV sums of the segments of cut columns
+    scratch_cap, scratch = 0, None
+    if index.segments is not None and index.seg_cap > index.num_blocks:
+        scratch_cap = 2 * (index.seg_cap - index.num_blocks)
+        scratch = torch.empty(rows * h_kv * scratch_cap * 2 * cfg.block_size * d,
+                              device=dev, dtype=torch.float32)
+    _lib.call("moba_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(dout),
+              _lib.ptr(lse_delta), _lib.ptr(index.col_nnz),
+              _lib.ptr(index.col_offsets), _lib.ptr(index.row_indices),
+              _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
+              _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),
+              _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d, index.num_blocks,
+              cfg.block_size, index.max_slots, index.row_indices.shape[-1], index_stride(index),
+              _lib.ptr(index.segments), _lib.ptr(index.seg_split), _lib.ptr(index.seg_counts),
+              index.seg_cap, _lib.ptr(scratch), scratch_cap, int(bool(causal)),
+              _lib.DTYPE_CODE[q.dtype], _lib.DTYPE_CODE[dq_part.dtype],
+              _lib.stream_handle(dev))
+
+
 def moba_backward(dout, q, k, v, out, lse, part_m, cfg: MoBAConfig, index: CSCIndex,
                   causal: bool = True):
     """Gradients of the MoBA forward (`moba_bwd.py:506-579`).
@@ -59,23 +88,11 @@ def moba_backward(dout, q, k, v, out, lse, part_m, cfg: MoBAConfig, index: CSCIn
     h_kv = k.shape[2]
     head_group_size(h_q, h_kv)
     dev = _lib.require_gpu(dout, q, k, v, out, lse, part_m)
-    slots = index.max_slots
     q, k, v = (_lib.aligned_contiguous(t) for t in (q, k, v))
     dout = _lib.aligned_contiguous(dout.to(q.dtype))
     lse_delta = compute_delta(out, dout, lse)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    dq_part = torch.empty((b, h_q, s, slots, d), device=dev, dtype=q.dtype)
-    rows = index.col_nnz.shape[0]
-    mx = index.max_seqlen if index.cu_seqlens is not None else s
-    _lib.call("moba_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(dout),
-              _lib.ptr(lse_delta), _lib.ptr(index.col_nnz),
-              _lib.ptr(index.col_offsets), _lib.ptr(index.row_indices),
-              _lib.ptr(index.head_indices), _lib.ptr(index.slot_of_pair),
-              _lib.ptr(index.order), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dq_part),
-              _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d, index.num_blocks,
-              cfg.block_size, slots, index.row_indices.shape[-1], index_stride(index),
-              int(bool(causal)),
-              _lib.DTYPE_CODE[q.dtype], _lib.DTYPE_CODE[dq_part.dtype],
-              _lib.stream_handle(dev))
+    dq_part = torch.empty((b, h_q, s, index.max_slots, d), device=dev, dtype=q.dtype)
+    bwd_kernel(dout, q, k, v, lse_delta, cfg, index, dk, dv, dq_part, causal=causal)
     return reduce_dq(dq_part, part_m, q.dtype), dk, dv

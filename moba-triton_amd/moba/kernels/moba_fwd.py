@@ -88,7 +88,9 @@ def attend_partials(q, k, v, cfg: MoBAConfig, index: CSCIndex, causal: bool = Tr
               _lib.ptr(index.slot_of_pair), _lib.ptr(index.order),
               _lib.ptr(part_m), _lib.ptr(part_acc), _lib.ptr(index.cu_seqlens), rows, s, mx, h_q, h_kv, d,
               index.num_blocks, cfg.block_size, slots, index.row_indices.shape[-1],
-              index_stride(index), int(bool(causal)), _lib.DTYPE_CODE[q.dtype],
+              index_stride(index), _lib.ptr(index.segments), _lib.ptr(index.seg_split),
+              _lib.ptr(index.seg_counts), index.seg_cap,
+              int(bool(causal)), _lib.DTYPE_CODE[q.dtype],
               _lib.DTYPE_CODE[part_acc.dtype], _lib.stream_handle(dev))
     return part_m, part_l, part_acc
 

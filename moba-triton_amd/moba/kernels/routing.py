@@ -2,6 +2,8 @@
 
 from dataclasses import dataclass
 
+import os
+
 import torch
 
 from moba import _lib
@@ -43,6 +45,27 @@ class CSCIndex:
     num_query_heads: int
     cu_seqlens: torch.Tensor | None = None
     max_seqlen: int | None = None
+    # Segment list (this build's addition; None: one program per column).
+    segments: torch.Tensor | None = None     # [R, H_kv, seg_cap, 4] int32
+    seg_split: torch.Tensor | None = None    # [R, H_kv, seg_cap - nb] int32
+    seg_counts: torch.Tensor | None = None   # [R, H_kv, 2] int32
+    seg_cap: int = 0
+
+
+ENV_SEGMENT = "MOBA_SEGMENT_ENTRIES"
+MAX_SEGMENTS = 8
+
+
+def segment_entries(total_pairs: int) -> int:
+    """Longest column segment one program takes: half of one workgroup
+    slot's share of all (query, slot) pairs (about 1024 programs run at
+    once), at least 2048 -- so only columns that would outlast the other
+    programs are cut (none at S = 512K, the longest few at 64K).
+    `MOBA_SEGMENT_ENTRIES` overrides it; 0 turns cutting off."""
+    env = os.environ.get(ENV_SEGMENT)
+    if env is not None:
+        return int(env)
+    return max(2048, -(-total_pairs // 1024))
 
 
 def index_stride(index: CSCIndex) -> int:
@@ -105,18 +128,28 @@ def build_csc_from_indices(block_idx: torch.Tensor, num_blocks: int, cfg: MoBACo
     # into one memory sector. The three fields are strided views of it.
     entries = torch.empty(rows, h_kv, cap, 3, **i32)
     row_indices, head_indices, slot_of_pair = entries.unbind(-1)
+    seg_len = segment_entries(rows * h_q * rps * slots)
+    seg = split = counts = None
+    seg_cap = 0
+    if seg_len > 0:
+        seg_cap = num_blocks + -(-(group * rps * slots) // seg_len)
+        seg = torch.empty(rows, h_kv, seg_cap, 4, **i32)
+        split = torch.empty(rows, h_kv, seg_cap - num_blocks, **i32)
+        counts = torch.empty(rows, h_kv, 2, **i32)
     lib = _lib.load()
     ws_bytes = int(lib.moba_csc_workspace_size(rows, s, h_q, h_kv, num_blocks, slots))
     ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
     _lib.call("moba_csc_build", _lib.ptr(block_idx), _lib.ptr(col_nnz),
               _lib.ptr(col_offsets), _lib.ptr(row_indices), _lib.ptr(head_indices),
               _lib.ptr(slot_of_pair), _lib.ptr(order), _lib.ptr(cu_seqlens), rows, s,
-              rps, h_q, h_kv, num_blocks, slots, 3, _lib.ptr(ws), ws.numel(),
-              _lib.stream_handle(dev))
+              rps, h_q, h_kv, num_blocks, slots, 3, _lib.ptr(seg), _lib.ptr(split),
+              _lib.ptr(counts), seg_cap, max(seg_len, 1), MAX_SEGMENTS, _lib.ptr(ws),
+              ws.numel(), _lib.stream_handle(dev))
     return CSCIndex(col_nnz=col_nnz, col_offsets=col_offsets, row_indices=row_indices,
                     head_indices=head_indices, slot_of_pair=slot_of_pair, order=order,
                     num_blocks=num_blocks, max_slots=slots, num_query_heads=h_q,
-                    cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+                    cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, segments=seg,
+                    seg_split=split, seg_counts=counts, seg_cap=seg_cap)
 
 
 def build_csc_fused(q: torch.Tensor, k: torch.Tensor, cfg: MoBAConfig,

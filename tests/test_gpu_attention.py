@@ -299,3 +299,43 @@ def test_chunked_partials_packed(device, monkeypatch):
     monkeypatch.setenv(ENV_BUDGET, "1")
     chunked = moba_forward(q, k, v, cfg, cu_seqlens=cu, max_seqlen=1024)
     assert torch.equal(whole, chunked)
+
+
+@pytest.mark.parametrize("shape,h_kv,cu", [((1, 2048, 4, 64), 4, None), ((2, 1024, 8, 128), 2, None),
+                                           ((1, 2048, 4, 64), 4, [0, 640, 1024, 2048])])
+def test_cut_columns_equal_whole_columns(device, monkeypatch, shape, h_kv, cu):
+    """Columns cut into segments (64 entries each, up to 8 per column) give
+    the forward and dQ of whole columns bit for bit (every (query, slot)
+    result comes from one program either way); dK / dV of cut columns are
+    float32 sums of the segments added in order, within the bf16 bars of the
+    whole-column result, and repeatable."""
+    from moba.kernels.routing import ENV_SEGMENT
+
+    q, k, v, do = make_qkv(shape, torch.bfloat16, seed=9, n=4)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    cfg = MoBAConfig(block_size=128, top_k=4)
+    qg, kg, vg, dog = (t.to(device) for t in (q, k, v, do))
+    cug = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=device)
+    mx = None if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
+
+    def run(index=None):
+        if index is None:
+            index = build_csc_fused(qg, kg, cfg, cu_seqlens=cug, max_seqlen=mx)
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (qg, kg, vg))
+        out = moba_attention(qq, kk, vv, cfg, index=index)
+        out.backward(dog)
+        return index, out.detach(), qq.grad, kk.grad, vv.grad
+
+    monkeypatch.setenv(ENV_SEGMENT, "0")
+    whole = run()
+    assert whole[0].segments is None
+    monkeypatch.setenv(ENV_SEGMENT, "64")
+    cut = run()
+    assert int(cut[0].seg_counts[..., 1].sum()) > 0, "no column was cut"
+    assert torch.equal(whole[1], cut[1]), "forward changed"
+    assert torch.equal(whole[2], cut[2]), "dQ changed"
+    for a, b in zip(whole[3:], cut[3:]):
+        assert max_abs_error(a.float(), b.float()) <= BF16_MAX_ABS
+        assert mean_abs_error(a.float(), b.float()) <= BF16_MEAN_ABS
+    again = run(cut[0])  # repeatable given the index (its column order is not fixed)
+    assert torch.equal(cut[3], again[3]) and torch.equal(cut[4], again[4])
