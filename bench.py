@@ -40,7 +40,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_fwd_bwd_S524288.json"
 # Stage -> the kernel that dominates it (name as rocprofv3 reports it).
 STAGE_KERNEL = {
-    "pool": "pool_kernel", "gate": "gate_mfma_kernel", "csc": "tile_count_or_scatter_kernel",
+    "pool": "pool_kernel", "gate": "gate_mfma_kernel", "csc": "det_scatter_kernel",
     "attend": "attend_mfma_kernel", "combine": "combine_kernel", "delta": "delta_kernel",
     "bwd": "bwd_mfma_kernel", "dq_reduce": "dq_reduce_kernel",
 }

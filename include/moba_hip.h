@@ -47,10 +47,12 @@ enum moba_status {
 
 enum moba_dtype { MOBA_BF16 = 0, MOBA_FP16 = 1, MOBA_FP32 = 2 };
 
-/* Library identity. moba_abi_version() is 4: (m, l) and (lse, delta) travel
- * as 8-byte pairs, the CSC index arrays take an element stride, and the CSC
- * build can emit a segment list that attend and backward take (version 1
- * took separate statistics arrays; 2 had no index stride; 3 no segments). */
+/* Library identity. moba_abi_version() is 5: (m, l) and (lse, delta) travel
+ * as 8-byte pairs, the CSC index arrays take an element stride, the CSC
+ * build can emit a segment list that attend and backward take, and its
+ * workspace is sized by rows per sequence (version 1 took separate
+ * statistics arrays; 2 had no index stride; 3 no segments; 4 sized the CSC
+ * workspace by seq_len and ordered column entries by atomic cursors). */
 int moba_abi_version(void);
 const char* moba_last_error(void);
 const char* moba_status_string(int status);
@@ -92,10 +94,13 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * col_nnz [R, Hkv, nb], col_offsets [R, Hkv, nb + 1] (exclusive prefix
  * sum), row_indices / head_indices / slot_of_pair [R, Hkv, cap] with
  * cap = (Hq / Hkv) * rows_per_seq * slots, order [R, Hkv, nb] (column ids by
- * count desc, id asc). Entries claim their position within a column with
- * an atomic cursor, so their order inside a column is unspecified (as in the
- * reference, routing.py:35-52); each (query, slot) pair appears exactly
- * once. row_indices hold packed token indices when cu_seqlens is given.
+ * count desc, id asc). Each (query, slot) pair appears exactly once. With
+ * nb <= 16384 a column's entries are in (query head, row) order -- the
+ * order of the dense-mask builder, routing.py:467-561 -- on every build, so
+ * the backward's dK / dV sums are bitwise reproducible; with more blocks
+ * they claim positions by atomic cursors and their order inside a column is
+ * unspecified (as in the reference's scatter, routing.py:35-52).
+ * row_indices hold packed token indices when cu_seqlens is given.
  * Ids outside [0, n_blocks), and ids past the last block a query of the
  * same 1024-query tile can see, are ignored like the -1 padding (moba_gate
  * never writes them; the guard keeps a bad caller buffer from addressing
@@ -116,7 +121,11 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * and its three kernels (routing.py:139-301); CSCIndex fields of
  * routing.py:73-130.
  */
-size_t moba_csc_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q,
+/* Workspace of moba_csc_build in bytes; rows_per_seq is seq_len, or
+ * max_seqlen when packed. For nb <= 16384 it holds a count table of
+ * R * Hq * ceil(rows_per_seq / 1024) * nb int32 plus chunk sums of
+ * R * Hkv * nb * (at most 64) int32; past that R * Hkv * nb int32 cursors. */
+size_t moba_csc_workspace_size(int64_t batch, int64_t rows_per_seq, int64_t h_q,
                                int64_t h_kv, int64_t n_blocks,
                                int64_t slots);
 int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,

@@ -2,15 +2,20 @@
 //
 // Restates src/moba/kernels/routing.py:139-301 (count / offsets+order /
 // scatter) and routing.py:309-427 (launcher): counts per (row, kv head,
-// block) with atomics, an exclusive scan into col_offsets, a longest-first
-// column order (count desc, id asc; the stable argsort of routing.py:548-553),
-// and an atomic-cursor scatter of (row, query head, slot) triples. Under GQA
-// every query head of a group lands in its kv head's columns.
+// block), an exclusive scan into col_offsets, a longest-first column order
+// (count desc, id asc; the stable argsort of routing.py:548-553), and a
+// scatter of (row, query head, slot) triples. Under GQA every query head of
+// a group lands in its kv head's columns. Up to kDetMaxCols (16384) columns
+// the scatter places a column's entries in (query head, row) order on every
+// build; past that it falls back to per-entry atomic cursors, whose order
+// within a column varies from run to run, as the reference's does.
 //
 // The order pass ranks each column directly -- rank = #columns with a larger
 // count, or the same count and a smaller id -- one lane per column against an
 // LDS copy of the counts. It is O(nb^2) work spread over nb lanes; at
 // nb = 4096 that is ~16M integer compares per head, a few microseconds.
+#include <mutex>
+
 #include "common.h"
 
 namespace moba {
@@ -57,15 +62,12 @@ count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __
   }
 }
 
-// Workgroup-aggregated variant: kTileQ queries of one (row, query head) per
-// workgroup, kTileT threads each taking kTileQ / kTileT of them. Selections
-// are first counted in an LDS histogram over the blocks this tile can see,
-// so the global counter of each block is touched once per workgroup -- the
-// own block, which every query of a block selects, would otherwise take 128
-// serialised global atomics, and a past block picked by several queries of
-// the tile takes one. Those per-(tile, block) atomics bound both passes, so
-// the tile is large. The scatter pass reserves each block's range with one
-// global atomic and hands out positions from LDS.
+// Tiled count: kTileQ queries of one (row, query head) per workgroup,
+// kTileT threads each taking kTileQ / kTileT of them, counted in an LDS
+// histogram over the blocks the tile can see and written out as one row of
+// the unit count table (below). The LDS histogram keeps the global memory
+// traffic at one row per tile: the own block, which every query of a block
+// selects, would otherwise take 128 serialised global atomics.
 constexpr int kTileQ = 1024;
 typedef int32_t i32x3 __attribute__((ext_vector_type(3), aligned(4)));
 constexpr int kTileT = 256;
@@ -74,43 +76,37 @@ constexpr int kMaxBins = 16384;
 // atomicAdd(&bins[blk], 1) for every active lane, with the lanes that share
 // the first active lane's id served by one atomic (every query of a block
 // selects its own block, so a wave's 64 consecutive queries usually agree
-// there); returns the old value plus the lane's rank among them.
-__device__ inline int32_t bin_add(int32_t* bins, int32_t blk, bool active) {
+// there).
+__device__ inline void bin_add(int32_t* bins, int32_t blk, bool active) {
   const uint64_t act = __ballot(active);
-  if (act == 0) return 0;
+  if (act == 0) return;
   const int lead = __builtin_ctzll(act);
   const int32_t b0 = __shfl(blk, lead);
   const bool same = active && blk == b0;
   const uint64_t m = __ballot(same);
   const int lane = threadIdx.x & 63;
-  const int32_t rank = __popcll(m & ((uint64_t(1) << lane) - 1));
-  int32_t base = 0;
-  if (lane == lead) base = atomicAdd(&bins[b0], __popcll(m));
-  base = __shfl(base, lead);
-  if (same) return base + rank;
-  return active ? atomicAdd(&bins[blk], 1) : 0;
+  if (lane == lead) atomicAdd(&bins[b0], __popcll(m));
+  if (active && !same) atomicAdd(&bins[blk], 1);
 }
 
-template <bool kScatter>
+// table row (rh * tiles + tile) = the tile's count of every column, zeros
+// where it sees none; grid (tiles, R * Hq).
 __global__ void __launch_bounds__(kTileT)
-tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
-                             const int32_t* __restrict__ cu, int64_t S, int64_t h_q,
-                             int64_t h_kv, int64_t n_blocks, int64_t bs, int slots,
-                             int64_t cap, int32_t* __restrict__ col_nnz_or_cursor,
-                             const int32_t* __restrict__ col_offsets,
-                             int32_t* __restrict__ row_indices,
-                             int32_t* __restrict__ head_indices,
-                             int32_t* __restrict__ slot_of_pair, int64_t istride,
-                             bool records) {
-  __shared__ int32_t bins[kMaxBins];
+tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restrict__ cu,
+                  int64_t S, int64_t h_q, int64_t n_blocks, int64_t bs, int slots,
+                  int32_t* __restrict__ table) {
+  extern __shared__ int32_t bins[];  // nb counters (dynamic LDS)
   const int64_t rh = blockIdx.y;
   const int64_t r = rh / h_q;
   const int64_t hq = rh % h_q;
-  const int64_t hk = hq / (h_q / h_kv);
   const bool packed = cu != nullptr;
   const SeqSpan sp = seq_span(cu, r, S);
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTileQ;
-  if (t0 >= sp.len) return;
+  int32_t* trow = table + (rh * gridDim.x + blockIdx.x) * n_blocks;
+  if (t0 >= sp.len) {
+    for (int64_t b = threadIdx.x; b < n_blocks; b += kTileT) trow[b] = 0;
+    return;
+  }
   const int64_t t_last = (t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len) - 1;
   const int64_t nv = t_last / bs + 1;  // blocks any query here can select
   const int nvis = static_cast<int>(nv < n_blocks ? nv : n_blocks);
@@ -118,50 +114,208 @@ tile_count_or_scatter_kernel(const int32_t* __restrict__ block_idx,
   __syncthreads();
   // Query i of this thread: t0 + threadIdx.x + kTileT * i (a wave's lanes
   // hold consecutive queries).
-  auto query = [&](int i, int64_t& t, int64_t& tok, int64_t& qid) {
-    t = t0 + threadIdx.x + kTileT * i;
-    tok = sp.bos + t;
-    qid = packed ? hq * S + tok : (r * h_q + hq) * S + t;
-    return t < sp.len;
-  };
   for (int i = 0; i < kTileQ / kTileT; ++i) {
-    int64_t t, tok, qid;
-    const bool live = query(i, t, tok, qid);
+    const int64_t t = t0 + threadIdx.x + kTileT * i;
+    const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
     for (int j = 0; j < slots; ++j) {
-      const int32_t blk = live ? block_idx[qid * slots + j] : -1;
+      const int32_t blk = t < sp.len ? block_idx[qid * slots + j] : -1;
       bin_add(bins, blk, blk >= 0 && blk < nvis);
     }
   }
   __syncthreads();
-  const int64_t colbase = (r * h_kv + hk) * n_blocks;
-  const int64_t obase = (r * h_kv + hk) * (n_blocks + 1);
-  for (int b = threadIdx.x; b < nvis; b += kTileT) {
-    const int32_t n = bins[b];
-    if (n > 0) {
-      const int32_t base = atomicAdd(&col_nnz_or_cursor[colbase + b], n);
-      // The scatter hands out positions from the column's start directly.
-      if (kScatter) bins[b] = col_offsets[obase + b] + base;
+  for (int64_t b = threadIdx.x; b < n_blocks; b += kTileT) trow[b] = b < nvis ? bins[b] : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic column order. Entries of a column are placed by (query head
+// within the group, query position), the order of the dense-mask CSC build
+// (routing.py:467-561 builds from mask.nonzero(), which walks that order),
+// so the index -- and with it the order in which the backward sums a
+// column's dK / dV -- is the same on every build.
+//
+// A unit is one (row, query head, 1024-query tile); the units of one
+// (row, kv head) in (query head, tile) order are exactly the column order.
+// The count pass writes each unit's per-column counts to a table
+// [R, Hq, tiles, nb]; a two-level exclusive scan over the units turns it
+// into each unit's first position per column (chunks of units are summed,
+// the chunk sums scanned, then each chunk rescanned from its base), and the
+// scatter hands out positions inside a unit in entry order.
+
+// Units of (row, kv head) rhk: (r * Hq + hk * G) * tiles + [0, G * tiles).
+// kPhase 0: csum[rhk, c, b] = sum of the chunk's counts of column b.
+// kPhase 1: table[u, b] = col_offsets[b] + csum[rhk, c, b] + exclusive sum
+// of the chunk's earlier units (csum holding chunk bases by then).
+template <int kPhase>
+__global__ void __launch_bounds__(256)
+unit_chunk_kernel(int32_t* __restrict__ table, int32_t* __restrict__ csum,
+                  const int32_t* __restrict__ col_offsets, int64_t n_blocks, int64_t h_q,
+                  int64_t h_kv, int64_t units, int64_t chunk, int64_t nchunks) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t c = blockIdx.y;
+  const int64_t rhk = blockIdx.z;
+  if (b >= n_blocks) return;
+  const int64_t r = rhk / h_kv, hk = rhk % h_kv;
+  const int64_t u0 = (r * h_q + hk * (h_q / h_kv)) * (units / (h_q / h_kv)) + c * chunk;
+  const int64_t u1 = c * chunk + chunk < units ? u0 + chunk : u0 + (units - c * chunk);
+  int32_t* cs = csum + (rhk * nchunks + c) * n_blocks + b;
+  if (kPhase == 0) {
+    int32_t acc = 0;
+    for (int64_t u = u0; u < u1; ++u) acc += table[u * n_blocks + b];
+    *cs = acc;
+  } else {
+    int32_t run = col_offsets[rhk * (n_blocks + 1) + b] + *cs;
+    for (int64_t u = u0; u < u1; ++u) {
+      const int32_t v = table[u * n_blocks + b];
+      table[u * n_blocks + b] = run;
+      run += v;
     }
   }
-  if (!kScatter) return;
-  __syncthreads();
+}
+
+// csum[rhk, :, b] -> exclusive scan over the chunks; the total is the
+// column's count.
+__global__ void __launch_bounds__(256)
+chunk_scan_kernel(int32_t* __restrict__ csum, int32_t* __restrict__ col_nnz, int64_t n_blocks,
+                  int64_t nchunks) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t rhk = blockIdx.y;
+  if (b >= n_blocks) return;
+  int32_t run = 0;
+  for (int64_t c = 0; c < nchunks; ++c) {
+    int32_t* p = csum + (rhk * nchunks + c) * n_blocks + b;
+    const int32_t v = *p;
+    *p = run;
+    run += v;
+  }
+  col_nnz[rhk * n_blocks + b] = run;
+}
+
+// One wave per unit. Its entries (query t, slot j) are contiguous in
+// block_idx and are taken 64 at a time (a "row" of the unit, lane l holding
+// entry 64 u + l). For each row, with i = t minus the row's first query
+// (i < 32: a row spans at most 32 queries when slots >= 2; with one slot a
+// row goes as two halves of 32):
+//   1. every entry (query offset i, column c) ORs bit i into c's LDS mask --
+//      an OR, so the result does not depend on the order of the lanes;
+//   2. its position is c's cursor plus the number of mask bits below bit i
+//      (the row's earlier queries holding c);
+//   3. the row's lowest query holding c (the only one with no mask bit below
+//      its own) advances c's cursor by the mask's popcount and clears the
+//      mask.
+// A query holds a column at most once, and a query split between two rows
+// holds each column in only one of them, so this places every column's
+// entries in query order, on every run.
+// Ids are prefetched a stage of kPer rows ahead into registers: a wave's
+// global stores share its load counter, so a load waited on between the
+// stores would also wait for every store before it.
+// Dynamic LDS: (cursor, mask) pairs of nb columns.
+constexpr int kPer = 16;
+// Columns the deterministic build handles (8 bytes of LDS each).
+constexpr int kDetMaxCols = kMaxBins;
+constexpr size_t kDetLdsBytes = 8 * static_cast<size_t>(kDetMaxCols);
+__global__ void __launch_bounds__(64)
+det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restrict__ cu,
+                   int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int64_t bs,
+                   int slots, int64_t cap, const int32_t* __restrict__ table,
+                   int32_t* __restrict__ row_indices, int32_t* __restrict__ head_indices,
+                   int32_t* __restrict__ slot_of_pair, int64_t istride, bool records) {
+  extern __shared__ uint32_t cm[];  // (cursor, mask) per column
+  const int64_t tile = blockIdx.x;
+  const int64_t rh = blockIdx.y;
+  const int64_t unit = rh * gridDim.x + tile;
+  const int64_t r = rh / h_q;
+  const int64_t hq = rh % h_q;
+  const int64_t hk = hq / (h_q / h_kv);
+  const bool packed = cu != nullptr;
+  const SeqSpan sp = seq_span(cu, r, S);
+  const int64_t t0 = tile * kTileQ;
+  if (t0 >= sp.len) return;
+  const int64_t t1 = t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len;
+  const int64_t nv = (t1 - 1) / bs + 1;
+  const int nvis = static_cast<int>(nv < n_blocks ? nv : n_blocks);
+  const int32_t* trow = table + unit * n_blocks;
+  const int lane = threadIdx.x;
+  for (int b0 = 0; b0 < nvis; b0 += 16 * 64) {  // 16 loads in flight per lane
+    int32_t v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int b = b0 + u * 64 + lane;
+      v[u] = b < nvis ? trow[b] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int b = b0 + u * 64 + lane;
+      if (b < nvis) {
+        cm[2 * b] = static_cast<uint32_t>(v[u]);
+        cm[2 * b + 1] = 0u;
+      }
+    }
+  }
+  // block_idx row of query t0 of this (row, head); entries run to t1.
+  const int64_t q0 = packed ? hq * S + sp.bos + t0 : (r * h_q + hq) * S + t0;
+  const int32_t* src = block_idx + q0 * slots;
+  const int32_t n_ent = static_cast<int32_t>((t1 - t0) * slots);
   const int64_t ibase = (r * h_kv + hk) * cap;
-  for (int i = 0; i < kTileQ / kTileT; ++i) {
-    int64_t t, tok, qid;
-    const bool live = query(i, t, tok, qid);
-    for (int j = 0; j < slots; ++j) {
-      const int32_t blk = live ? block_idx[qid * slots + j] : -1;
-      const bool ok = blk >= 0 && blk < nvis;
-      const int32_t pos = bin_add(bins, blk, ok);
-      if (!ok) continue;
-      const int64_t dst = (ibase + pos) * istride;
-      const int32_t rv = static_cast<int32_t>(packed ? tok : t);
-      if (records) {  // (row, head, slot) adjacent: one 12-byte store
-        *reinterpret_cast<i32x3*>(row_indices + dst) = i32x3{rv, static_cast<int32_t>(hq), j};
-      } else {
-        row_indices[dst] = rv;
-        head_indices[dst] = static_cast<int32_t>(hq);
-        slot_of_pair[dst] = j;
+  const int32_t rbase = static_cast<int32_t>(packed ? sp.bos + t0 : t0);
+  // Lane's entry of the current row: query q (from t0), slot j; stepped by
+  // 64 entries per row without division.
+  int32_t q = lane / slots, j = lane % slots;
+  const int32_t dq = 64 / slots, dj = 64 % slots;
+  const int halves = slots == 1 ? 2 : 1;
+  int32_t cur[kPer], nxt[kPer];
+  auto fetch = [&](int32_t* dst, int32_t s0) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int32_t e = s0 + u * 64 + lane;
+      dst[u] = e < n_ent ? src[e] : -1;
+    }
+  };
+  fetch(nxt, 0);
+  for (int32_t s0 = 0; s0 < n_ent; s0 += kPer * 64) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) cur[u] = nxt[u];
+    if (s0 + kPer * 64 < n_ent) fetch(nxt, s0 + kPer * 64);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      if (s0 + u * 64 < n_ent) {
+        const int32_t blk = cur[u];
+        const bool valid = blk >= 0 && blk < nvis;
+        for (int h = 0; h < halves; ++h) {
+          const bool ok = valid && (halves == 1 || (lane >> 5) == h);
+          const int32_t qrow = __builtin_amdgcn_readlane(q, h * 32);
+          const uint32_t bit = static_cast<uint32_t>(q - qrow);
+          const uint32_t lower = (1u << bit) - 1u;
+          if (ok)
+            __hip_atomic_fetch_or(&cm[2 * blk + 1], 1u << bit, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+          uint32_t c = 0, m = 0;
+          if (ok) {
+            c = cm[2 * blk];
+            m = cm[2 * blk + 1];
+          }
+          if (ok && (m & lower) == 0u) {
+            cm[2 * blk] = c + __popc(m);
+            cm[2 * blk + 1] = 0u;
+          }
+          if (ok) {
+            const int32_t pos = static_cast<int32_t>(c) + __popc(m & lower);
+            const int64_t dst = (ibase + pos) * istride;
+            if (records) {
+              *reinterpret_cast<i32x3*>(row_indices + dst) =
+                  i32x3{rbase + q, static_cast<int32_t>(hq), j};
+            } else {
+              row_indices[dst] = rbase + q;
+              head_indices[dst] = static_cast<int32_t>(hq);
+              slot_of_pair[dst] = j;
+            }
+          }
+        }
+      }
+      q += dq;
+      j += dj;
+      if (j >= slots) {
+        j -= slots;
+        ++q;
       }
     }
   }
@@ -302,10 +456,48 @@ seg_build_kernel(const int32_t* __restrict__ col_nnz, const int32_t* __restrict_
 
 }  // namespace moba
 
-extern "C" size_t moba_csc_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q,
+namespace {
+// Deterministic-build geometry: units of one (row, kv head) and their chunks.
+struct UnitPlan {
+  int64_t tiles, units, chunk, nchunks;
+};
+UnitPlan unit_plan(int64_t rows_per_seq, int64_t h_q, int64_t h_kv) {
+  UnitPlan p;
+  p.tiles = moba::cdiv(rows_per_seq, moba::kTileQ);
+  p.units = (h_kv > 0 ? h_q / h_kv : 1) * p.tiles;
+  p.chunk = moba::cdiv(p.units, 64) > 16 ? moba::cdiv(p.units, 64) : 16;
+  p.nchunks = moba::cdiv(p.units, p.chunk);
+  return p;
+}
+// True when det_scatter_kernel may take `bytes` of dynamic LDS on the
+// current device: always up to 64 KiB; beyond that when the device's opt-in
+// limit allows it, after raising the kernel's limit once per process.
+bool det_lds_ok(size_t bytes) {
+  if (bytes <= 65536) return true;
+  int dev = 0, optin = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&optin, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess ||
+      static_cast<size_t>(optin) < bytes)
+    return false;
+  static std::once_flag once;
+  static bool raised = false;
+  std::call_once(once, [] {
+    raised = hipFuncSetAttribute(reinterpret_cast<const void*>(moba::det_scatter_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(moba::kDetLdsBytes)) == hipSuccess;
+  });
+  return raised;
+}
+}  // namespace
+
+extern "C" size_t moba_csc_workspace_size(int64_t batch, int64_t rows_per_seq, int64_t h_q,
                                           int64_t h_kv, int64_t n_blocks, int64_t slots) {
-  (void)seq_len; (void)h_q; (void)slots;
-  return sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n_blocks);
+  (void)slots;
+  if (n_blocks > moba::kDetMaxCols)  // atomic cursors of the untiled build
+    return sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n_blocks);
+  const UnitPlan p = unit_plan(rows_per_seq, h_q, h_kv);
+  return sizeof(int32_t) * static_cast<size_t>(batch * n_blocks *
+                                               (h_q * p.tiles + h_kv * p.nchunks));
 }
 
 extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
@@ -333,57 +525,71 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   if (!block_idx || !col_nnz || !col_offsets || !row_indices || !head_indices ||
       !slot_of_pair || !order)
     return fail(MOBA_ERR_INVALID, "null pointer");
-  const size_t need = moba_csc_workspace_size(batch, seq_len, h_q, h_kv, n_blocks, slots);
+  const size_t need = moba_csc_workspace_size(batch, rps, h_q, h_kv, n_blocks, slots);
   if (!workspace || workspace_bytes < need)
     return fail(MOBA_ERR_WORKSPACE, "csc workspace too small");
   const int64_t cap = g.group * g.rows_per_seq * slots;
   if (cap >= (int64_t(1) << 31))
     return fail(MOBA_ERR_UNSUPPORTED, "column capacity exceeds int32 offsets");
   hipStream_t s = as_stream(stream);
-  int32_t* cursor = static_cast<int32_t*>(workspace);
   const bool records = index_stride == 3 && head_indices == row_indices + 1 &&
                        slot_of_pair == row_indices + 2;
   const int64_t ncols = batch * h_kv * n_blocks;
   const unsigned fill_blocks = static_cast<unsigned>(cdiv(ncols, 256) < 4096 ? cdiv(ncols, 256) : 4096);
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, col_nnz, ncols, 0);
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, cursor, ncols, 0);
   // A lower bound on the block size: cdiv(rows, n_blocks) <= block_size, so
   // t / bs_eff never under-counts the blocks a query can see.
-  const bool tiled = n_blocks <= kMaxBins;
+  const size_t det_lds = 8 * static_cast<size_t>(n_blocks);
+  const bool tiled = n_blocks <= kDetMaxCols && det_lds_ok(det_lds);
   const int64_t bs_eff = cdiv(g.rows_per_seq, n_blocks);
+  const UnitPlan up = unit_plan(g.rows_per_seq, h_q, h_kv);
+  const unsigned col_groups = static_cast<unsigned>(cdiv(n_blocks, 256));
+  const unsigned rhk = static_cast<unsigned>(batch * h_kv);
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq * slots, 256)),
             static_cast<unsigned>(batch * h_q));
-  dim3 tgrid(static_cast<unsigned>(cdiv(g.rows_per_seq, kTileQ)),
-             static_cast<unsigned>(batch * h_q));
-  if (tiled)
-    hipLaunchKernelGGL(tile_count_or_scatter_kernel<false>, tgrid, dim3(kTileT), 0, s,
-                       block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
-                       static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
-                       nullptr, index_stride, false);
-  else
+  dim3 tgrid(static_cast<unsigned>(up.tiles), static_cast<unsigned>(batch * h_q));
+  int32_t* table = static_cast<int32_t*>(workspace);
+  int32_t* csum = table + batch * h_q * up.tiles * n_blocks;
+  int32_t* cursor = static_cast<int32_t*>(workspace);
+  if (tiled) {
+    // Deterministic build: per-unit counts, scanned into per-unit bases.
+    hipLaunchKernelGGL(tile_count_kernel, tgrid, dim3(kTileT),
+                       static_cast<unsigned>(sizeof(int32_t) * n_blocks), s, block_idx, cu_seqlens,
+                       seq_len, h_q, n_blocks, bs_eff, static_cast<int>(slots), table);
+    hipLaunchKernelGGL(unit_chunk_kernel<0>,
+                       dim3(col_groups, static_cast<unsigned>(up.nchunks), rhk), dim3(256), 0,
+                       s, table, csum, nullptr, n_blocks, h_q, h_kv, up.units, up.chunk,
+                       up.nchunks);
+    hipLaunchKernelGGL(chunk_scan_kernel, dim3(col_groups, rhk), dim3(256), 0, s, csum,
+                       col_nnz, n_blocks, up.nchunks);
+  } else {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, col_nnz, ncols, 0);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, cursor, ncols, 0);
     hipLaunchKernelGGL(count_or_scatter_kernel<false>, grid, dim3(256), 0, s, block_idx,
                        cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
                        static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
                        nullptr, index_stride);
-  hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024), 0, s,
-                     col_nnz, col_offsets, n_blocks);
-  hipLaunchKernelGGL(order_kernel,
-                     dim3(static_cast<unsigned>(cdiv(n_blocks, 32)),
-                          static_cast<unsigned>(batch * h_kv)),
+  }
+  hipLaunchKernelGGL(scan_kernel, dim3(rhk), dim3(1024), 0, s, col_nnz, col_offsets, n_blocks);
+  hipLaunchKernelGGL(order_kernel, dim3(static_cast<unsigned>(cdiv(n_blocks, 32)), rhk),
                      dim3(256), 0, s, col_nnz, order, n_blocks);
   if (segments)
-    hipLaunchKernelGGL(seg_build_kernel, dim3(static_cast<unsigned>(batch * h_kv)), dim3(1024),
-                       0, s, col_nnz, order, n_blocks, seg_len, static_cast<int>(max_seg),
-                       segments, seg_split, seg_counts, seg_cap);
-  if (tiled)
-    hipLaunchKernelGGL(tile_count_or_scatter_kernel<true>, tgrid, dim3(kTileT), 0, s,
-                       block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
-                       static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
-                       head_indices, slot_of_pair, index_stride, records);
-  else
+    hipLaunchKernelGGL(seg_build_kernel, dim3(rhk), dim3(1024), 0, s, col_nnz, order, n_blocks,
+                       seg_len, static_cast<int>(max_seg), segments, seg_split, seg_counts,
+                       seg_cap);
+  if (tiled) {
+    hipLaunchKernelGGL(unit_chunk_kernel<1>,
+                       dim3(col_groups, static_cast<unsigned>(up.nchunks), rhk), dim3(256), 0,
+                       s, table, csum, col_offsets, n_blocks, h_q, h_kv, up.units, up.chunk,
+                       up.nchunks);
+    hipLaunchKernelGGL(det_scatter_kernel, tgrid, dim3(64),
+                       static_cast<unsigned>(det_lds), s, block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
+                       static_cast<int>(slots), cap, table, row_indices, head_indices,
+                       slot_of_pair, index_stride, records);
+  } else {
     hipLaunchKernelGGL(count_or_scatter_kernel<true>, grid, dim3(256), 0, s, block_idx,
                        cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
                        static_cast<int>(slots), cap, cursor, col_offsets, row_indices,
                        head_indices, slot_of_pair, index_stride);
+  }
   return check_launch("moba_csc_build");
 }

@@ -55,6 +55,10 @@ class LibraryMissing(RuntimeError):
     """The HIP library has not been built (or cannot be loaded)."""
 
 
+# Version of include/moba_hip.h these bindings follow.
+ABI_VERSION = 5
+
+
 def load() -> ctypes.CDLL:
     """Loads the library once and binds every declared signature."""
     global _lib
@@ -72,6 +76,10 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.moba_abi_version() != ABI_VERSION:
+        raise LibraryMissing(
+            f"{LIB_PATH} has ABI version {lib.moba_abi_version()}, these bindings expect "
+            f"{ABI_VERSION}; rebuild it")
     _lib = lib
     return lib
 

@@ -137,7 +137,7 @@ def build_csc_from_indices(block_idx: torch.Tensor, num_blocks: int, cfg: MoBACo
         split = torch.empty(rows, h_kv, seg_cap - num_blocks, **i32)
         counts = torch.empty(rows, h_kv, 2, **i32)
     lib = _lib.load()
-    ws_bytes = int(lib.moba_csc_workspace_size(rows, s, h_q, h_kv, num_blocks, slots))
+    ws_bytes = int(lib.moba_csc_workspace_size(rows, rps, h_q, h_kv, num_blocks, slots))
     ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
     _lib.call("moba_csc_build", _lib.ptr(block_idx), _lib.ptr(col_nnz),
               _lib.ptr(col_offsets), _lib.ptr(row_indices), _lib.ptr(head_indices),

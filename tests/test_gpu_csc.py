@@ -33,6 +33,14 @@ def test_csc_matches_reference_builder(device, b, s, hq, hkv, bs, tk):
     assert torch.equal(index.col_offsets.cpu(), ref["col_offsets"])
     assert torch.equal(index.order.cpu(), ref["order"]), "longest-first order differs"
     assert torch.equal(csc_to_mask(index, s).cpu(), sel)
+    # every entry in place: the build orders a column by (query head, row),
+    # as the dense-mask builder does
+    for f in ("row_indices", "head_indices", "slot_of_pair"):
+        for bi in range(b):
+            for kv in range(hkv):
+                tot = int(ref["col_offsets"][bi, kv, -1])
+                assert torch.equal(getattr(index, f)[bi, kv, :tot].cpu(),
+                                   ref[f][bi, kv, :tot]), f
     # column membership as a set of (head, row, slot), including slot numbers
     ic = type(index)(**{f: (getattr(index, f).cpu() if torch.is_tensor(getattr(index, f))
                             else getattr(index, f)) for f in index.__dataclass_fields__})
@@ -113,3 +121,107 @@ def test_csc_ignores_ids_no_query_can_hold(device):
     for blk in range(nb):
         assert column_sets(got, 0, 0, blk) == column_sets(want, 0, 0, blk)
         assert column_sets(got, 0, 1, blk) == column_sets(want, 0, 1, blk)
+
+
+def synthetic_ids(rows, h_q, s, slots, bs_eff, seed, lens=None):
+    """Distinct valid ids per query, causal at block size bs_eff (-1 padded
+    when a query can see fewer than `slots` blocks)."""
+    g = torch.Generator().manual_seed(seed)
+    t = torch.arange(s)
+    if lens is not None:  # packed: position within the query's own sequence
+        starts = torch.repeat_interleave(torch.tensor([0] + lens[:-1]).cumsum(0),
+                                         torch.tensor(lens))
+        t = t - starts
+    vis = (t // bs_eff + 1).view(1, 1, s, 1)
+    keys = torch.rand(rows, h_q, s, 4 * slots, generator=g)
+    cand = (keys * vis).long()  # in [0, vis)
+    idx = torch.full((rows, h_q, s, slots), -1, dtype=torch.long)
+    for j in range(4 * slots):  # first `slots` distinct candidates
+        c = cand[..., j:j + 1]
+        fresh = ~(idx == c).any(-1, keepdim=True)
+        free = (idx == -1).int().argmax(-1, keepdim=True)
+        room = (idx == -1).any(-1, keepdim=True)
+        put = fresh & room
+        idx.scatter_(-1, free, torch.where(put, c, idx.gather(-1, free)))
+    return idx.to(torch.int32)
+
+
+def canonical(block_idx, nb, h_kv, cu=None):
+    """Per (row, kv head): the (block, head, row, slot) of every entry in
+    (block, query head, row) order -- computed with torch sorts."""
+    rows, h_q, s, slots = block_idx.shape
+    if cu is not None:
+        rows = cu.numel() - 1
+    g = h_q // h_kv
+    out = {}
+    for r in range(rows):
+        for kv in range(h_kv):
+            ids = []
+            for hh in range(kv * g, kv * g + g):
+                if cu is None:
+                    bi = block_idx[r, hh]
+                    tok = torch.arange(s)
+                else:
+                    lo, hi = int(cu[r]), int(cu[r + 1])
+                    bi = block_idx[0, hh, lo:hi]
+                    tok = torch.arange(lo, hi)
+                q, j = (bi >= 0).nonzero(as_tuple=True)
+                ids.append(torch.stack([bi[q, j].long(), torch.full_like(q, hh), tok[q], j], 1))
+            e = torch.cat(ids)
+            key = (e[:, 0] * h_q + e[:, 1]) * (1 << 40) + e[:, 2]
+            out[(r, kv)] = e[key.argsort(stable=True)]
+    return out
+
+
+def entries(index, r, kv):
+    tot = int(index.col_offsets[r, kv, -1])
+    nnz = index.col_nnz[r, kv].long().cpu()
+    blk = torch.repeat_interleave(torch.arange(nnz.numel()), nnz)
+    return torch.stack([blk, index.head_indices[r, kv, :tot].long().cpu(),
+                        index.row_indices[r, kv, :tot].long().cpu(),
+                        index.slot_of_pair[r, kv, :tot].long().cpu()], 1)
+
+
+@pytest.mark.parametrize("s,nb,packed", [(8000, 1000, False), (8000, 1000, True),
+                                         (24000, 12000, False),   # > 64 KiB of LDS
+                                         (40000, 20000, False)])  # atomic fallback
+def test_csc_column_order(device, s, nb, packed):
+    """Up to 16384 columns the entries of a column come in (query head, row)
+    order; past that (atomic cursors) the same entries in some order."""
+    h_q, h_kv, slots = 4, 2, 4
+    cfg = MoBAConfig(block_size=64, top_k=slots)
+    lens = [3000, 1000, 4000] if packed else None
+    rps = max(lens) if packed else s
+    bs_eff = -(-rps // nb)
+    idx = synthetic_ids(1 if packed else 2, h_q, s, slots, bs_eff, seed=11, lens=lens)
+    cu = torch.tensor([0, 3000, 4000, 8000], dtype=torch.int32) if packed else None
+    got = build_csc_from_indices(idx.to(device), nb, cfg, num_kv_heads=h_kv,
+                                 cu_seqlens=None if cu is None else cu.to(device),
+                                 max_seqlen=rps if packed else None)
+    want = canonical(idx, nb, h_kv, cu)
+    for (r, kv), w in want.items():
+        e = entries(got, r, kv)
+        if nb <= 16384:
+            assert torch.equal(e, w), (r, kv)
+        else:
+            k = lambda x: (x[:, 0] * h_q + x[:, 1]) * (1 << 40) + x[:, 2]
+            assert torch.equal(e[k(e).argsort()], w), (r, kv)
+
+
+def test_gradients_are_bitwise_stable_across_index_builds(device):
+    """Two separately built indexes give the same dQ, dK and dV bit for bit
+    (the backward sums a column in its entry order, which is fixed)."""
+    from moba.kernels.attention import moba_attention
+
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    q, k, v = make_qkv((1, 16384, 4, 64), torch.bfloat16, seed=4, device=device)
+    dout = torch.randn_like(q)
+    grads = []
+    for _ in range(2):
+        index = build_csc_fused(q, k, cfg)
+        qq, kk, vv = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+        out = moba_attention(qq, kk, vv, cfg, index=index)
+        out.backward(dout)
+        grads.append((out.detach(), qq.grad, kk.grad, vv.grad))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)

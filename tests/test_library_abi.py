@@ -20,7 +20,7 @@ def declared_functions():
 
 def test_library_loads():
     lib = _lib.load()
-    assert lib.moba_abi_version() == 4
+    assert lib.moba_abi_version() == 5
 
 
 def test_every_declared_symbol_is_exported_and_bound():
@@ -56,4 +56,8 @@ def test_invalid_arguments_fail_on_the_host():
 def test_workspace_queries_are_host_only():
     lib = _lib.load()
     assert lib.moba_gate_workspace_size(1, 65536, 4) >= 8 * 65536 * 4
-    assert lib.moba_csc_workspace_size(1, 65536, 4, 4, 512, 8) == 4 * 4 * 512
+    # count table: 4 heads x 64 tiles x 512 columns; chunk sums: 4 kv heads x
+    # 4 chunks (64 units in chunks of 16) x 512 columns
+    assert lib.moba_csc_workspace_size(1, 65536, 4, 4, 512, 8) == 4 * (4 * 64 + 4 * 4) * 512
+    # past 16384 columns: one atomic cursor per column
+    assert lib.moba_csc_workspace_size(2, 1 << 22, 4, 2, 32768, 8) == 4 * 2 * 2 * 32768
