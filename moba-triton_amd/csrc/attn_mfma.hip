@@ -55,18 +55,24 @@ __device__ inline V ld16(const void* p) {
 // Four consecutive elements in one store (8 bytes for 16-bit types).
 template <typename A>
 __device__ inline void store4(A* p, float x0, float x1, float x2, float x3);
+// Round to nearest even by the hardware conversions (v_cvt_pk_bf16_f32,
+// v_cvt_f16_f32): the same results as the integer rounding of common.h for
+// every finite input, without its per-value branches.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 template <>
 __device__ inline void store4<bf16_t>(bf16_t* p, float x0, float x1, float x2, float x3) {
   uint2 u;
-  u.x = float_to_bf16(x0) | (static_cast<uint32_t>(float_to_bf16(x1)) << 16);
-  u.y = float_to_bf16(x2) | (static_cast<uint32_t>(float_to_bf16(x3)) << 16);
+  u.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x0, x1}, bf16x2_t));
+  u.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x2, x3}, bf16x2_t));
   *reinterpret_cast<uint2*>(p) = u;
 }
 template <>
 __device__ inline void store4<f16_t>(f16_t* p, float x0, float x1, float x2, float x3) {
   uint2 u;
-  u.x = float_to_f16(x0) | (static_cast<uint32_t>(float_to_f16(x1)) << 16);
-  u.y = float_to_f16(x2) | (static_cast<uint32_t>(float_to_f16(x3)) << 16);
+  u.x = __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(x0), static_cast<_Float16>(x1)});
+  u.y = __builtin_bit_cast(uint32_t, f16x2_t{static_cast<_Float16>(x2), static_cast<_Float16>(x3)});
   *reinterpret_cast<uint2*>(p) = u;
 }
 template <>

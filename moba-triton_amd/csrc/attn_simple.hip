@@ -338,13 +338,25 @@ __device__ inline void load8<float>(const float* p, float (&x)[8]) {
   x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
   x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
+// 16-bit stores round to nearest even by the hardware conversions
+// (v_cvt_pk_bf16_f32, v_cvt_f16_f32): the integer rounding of common.h for
+// every finite input, without its per-value branches.
 template <typename A>
-__device__ inline void store8(A* p, const float (&x)[8]) {
-  uint4 u;
-  uint16_t* e = reinterpret_cast<uint16_t*>(&u);
+__device__ inline void store8(A* p, const float (&x)[8]);
+template <>
+__device__ inline void store8<bf16_t>(bf16_t* p, const float (&x)[8]) {
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+  typedef float f32x8_t __attribute__((ext_vector_type(8)));
+  const f32x8_t v = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+  *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, __builtin_convertvector(v, bf16x8_t));
+}
+template <>
+__device__ inline void store8<f16_t>(f16_t* p, const float (&x)[8]) {
+  typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+  f16x8_t h;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) Elem<A>::store(reinterpret_cast<A*>(e), i, x[i]);
-  *reinterpret_cast<uint4*>(p) = u;
+  for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(x[i]);
+  *reinterpret_cast<uint4*>(p) = __builtin_bit_cast(uint4, h);
 }
 template <>
 __device__ inline void store8<float>(float* p, const float (&x)[8]) {
