@@ -52,6 +52,21 @@ __device__ inline V ld16(const void* p) {
   return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes,
+// lane i receives element i % 4 of the 8-byte chunks that lanes i / 4,
+// 4 + i / 4, 8 + i / 4 and 12 + i / 4 address. Two of them give one 8-wide
+// MFMA operand whose elements run along the rows of a row-major tile.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+template <typename V>
+__device__ inline V ld_tr2(const uint16_t* p0, const uint16_t* p1) {
+  typedef __attribute__((address_space(3))) v4i16_t lds_v4i16;
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p0));
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p1));
+  typedef short v8i16_t __attribute__((ext_vector_type(8)));
+  const v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(V, v);
+}
+
 // Four consecutive elements in one store (8 bytes for 16-bit types).
 template <typename A>
 __device__ inline void store4(A* p, float x0, float x1, float x2, float x3);
@@ -369,14 +384,16 @@ int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hip
 // Backward (bwd_mfma_kernel): one workgroup per (KV block, row * kv head),
 // one wave per 32 keys of the block. The workgroup owns its keys' dK / dV
 // for the whole column (registers, stored once: no atomics), and walks the
-// column in steps of 64 entries. Per step, with the step's Q / dO staged
-// in LDS in both orientations:
+// column in steps of 64 entries. Per step, with the step's Q / dO rows
+// staged in LDS (row-major; the transposed operands come from transposing
+// reads, ds_read_b64_tr_b16):
 //
 //   S[q][key]   = Q . K^T,   dP[q][key] = dO . V^T      (lane <-> key)
 //   P = exp2(S * scale log2e - lse),  dS = P (dP - delta)
 //   dV^T[d][key] += dO^T . P,   dK^T[d][key] += Q^T . dS  (P, dS straight
 //                                                         from registers)
-//   dQ^T[d][q]   = K^T . dS^T over all keys of the block, via dS in LDS
+//   dQ^T[d][q]   = K^T . dS^T over all keys of the block, via dS^T rows
+//                  ([key][q], 8-byte writes) in LDS
 //
 // and writes one dQ partial per (query, slot) -- summed over the whole block
 // inside the workgroup, so the partial buffer is [.., slots, D], not
@@ -394,21 +411,12 @@ bwd_mfma_kernel(AttnArgs a) {
   constexpr int NT = NW * 64;   // threads
   constexpr int DT = D / 32;
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
-  constexpr int KTS = BS + 8;   // row stride of K^T and dS ([*][key])
-  constexpr int QTS = NQ + 8;   // row stride of Q^T / dO^T ([d][q])
-  // Element (feature d, permuted query position qp) of Q^T / dO^T. The
-  // 8-element chunks of a row are XOR-swizzled by d / 8, so the transposing
-  // writes of one query's eight features (rows d8 .. d8 + 7 for every d8)
-  // fall into distinct banks; 8-aligned runs stay contiguous for the reads.
-  auto tq = [](int d, int qp) {
-    return d * QTS + ((((qp >> 3) ^ ((d >> 3) % (NQ / 8))) << 3) | (qp & 7));
-  };
+  constexpr int KTS = BS + 8;   // row stride of K^T ([d][key])
+  constexpr int QS2 = NQ + 8;   // row stride of dS^T ([key][q])
   __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
   __shared__ __attribute__((aligned(16))) uint16_t Qs[NQ * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Os[NQ * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[D * QTS];
-  __shared__ __attribute__((aligned(16))) uint16_t Ot[D * QTS];
-  __shared__ __attribute__((aligned(16))) uint16_t DS[NQ * KTS];
+  __shared__ __attribute__((aligned(16))) uint16_t DSt[BS * QS2];
   __shared__ __attribute__((aligned(16))) float s_lse[NQ];
   __shared__ __attribute__((aligned(16))) float s_delta[NQ];
   __shared__ __attribute__((aligned(16))) int s_lim[NQ];
@@ -542,31 +550,14 @@ bwd_mfma_kernel(AttnArgs a) {
       s_delta[tid] = c_dl;
       s_dst[tid] = c_dst;
     }
-    // Q and dO rows: row-major and transposed (q permuted per 16-slice so
-    // each lane-half's eight queries of a K-step are contiguous).
+    // Q and dO rows, row-major; the dV / dK products read them transposed.
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = tid + u * NT;
       const int q = i / (D / 8);
       const int d8 = (i % (D / 8)) * 8;
-      const u32x4 vq = pv[u] ? pq[u] : u32x4{0, 0, 0, 0};
-      const u32x4 vo = pv[u] ? po[u] : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = vq;
-      *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = vo;
-      const uint16_t* qe = reinterpret_cast<const uint16_t*>(&vq);
-      const uint16_t* oe = reinterpret_cast<const uint16_t*>(&vo);
-      const int qp = (q & ~15) + perm16(q & 15);
-      // Rows d8 .. d8 + 7 share d8's swizzle (d8 is a multiple of 8), so the
-      // eight writes are one base plus immediate offsets.
-      int tb = tq(d8, qp);
-      // Opaque to loop-invariant hoisting: otherwise each of the 16 row
-      // addresses is hoisted into a register of its own for the whole column.
-      asm volatile("" : "+v"(tb));
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        Qt[tb + w * QTS] = qe[w];
-        Ot[tb + w * QTS] = oe[w];
-      }
+      *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = pv[u] ? pq[u] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = pv[u] ? po[u] : u32x4{0, 0, 0, 0};
     }
     __syncthreads();
     const bool more = g0 + NQ < c.n;
@@ -597,25 +588,37 @@ bwd_mfma_kernel(AttnArgs a) {
         const int limv[4] = {lim4.x, lim4.y, lim4.z, lim4.w};
         const float lsev[4] = {lse4.x, lse4.y, lse4.z, lse4.w};
         const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+        float dsf[4];  // this key's dS of the four queries: one 8-byte row piece
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const int v = 4 * g + w;
-          const int q = q0 + w;
           const float x = mykey <= limv[w] ? sacc[v] * a.scale_log2 - lsev[w] : -INFINITY;
           const float p = __builtin_amdgcn_exp2f(x);
           const float ds = p * (pacc[v] - dlv[w]);
           pb[v >> 3][v & 7] = static_cast<Sc>(p);
           db[v >> 3][v & 7] = static_cast<Sc>(ds);
-          DS[q * KTS + mykey] = __builtin_bit_cast(uint16_t, static_cast<Sc>(ds));
+          dsf[w] = ds;
         }
+        typedef Sc sc4_t __attribute__((ext_vector_type(4)));
+        typedef float f32x4_t __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<uint2*>(&DSt[mykey * QS2 + q0]) = __builtin_bit_cast(
+            uint2, __builtin_convertvector(f32x4_t{dsf[0], dsf[1], dsf[2], dsf[3]}, sc4_t));
       }
+      // dV^T += dO^T . P and dK^T += Q^T . dS. The A operands are dO / Q
+      // read transposed: lane (group g = lane / 16, r = lane % 16) addresses
+      // row 32qt + 16j + 8m + 4h + r / 4, features 32dt + 16(g % 2) + 4(r % 4)
+      // + [0, 4) for half m of the operand, so lane (col, h) receives
+      // feature 32dt + col of the queries 32qt + 16j + 8m + 4h + [0, 4) --
+      // the queries of its P / dS B operand elements 4m .. 4m + 3.
+      const int tr_row = 4 * h + ((lane & 15) >> 2);
+      const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int qoff = qt * 32 + 16 * j + 8 * h;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          dv[dt] = M::mma(ld16<V8>(&Ot[tq(dt * 32 + col, qoff)]), pb[j], dv[dt]);
-          dk[dt] = M::mma(ld16<V8>(&Qt[tq(dt * 32 + col, qoff)]), db[j], dk[dt]);
+          const int o0 = (qt * 32 + 16 * j + tr_row) * RS + dt * 32 + tr_col;
+          dv[dt] = M::mma(ld_tr2<V8>(&Os[o0], &Os[o0 + 8 * RS]), pb[j], dv[dt]);
+          dk[dt] = M::mma(ld_tr2<V8>(&Qs[o0], &Qs[o0 + 8 * RS]), db[j], dk[dt]);
         }
       }
     }
@@ -625,6 +628,11 @@ bwd_mfma_kernel(AttnArgs a) {
     // over the waves.
     constexpr int TPW = DT * QT / NW;
     static_assert(DT * QT % NW == 0, "dQ tiles must spread evenly over the waves");
+    // B operand (dS^T, keys 16j + 8h + [0, 8) of query 32qt + col) read
+    // transposed from the [key][q] rows: lane (g, r) addresses key
+    // 16j + 8h + 4m + r / 4, queries 32qt + 16(g % 2) + 4(r % 4) + [0, 4).
+    const int tr_key = 8 * h + ((lane & 15) >> 2);
+    const int tr_q = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     floatx16_t dq[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
@@ -634,7 +642,9 @@ bwd_mfma_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < BS / 16; ++j)
         dq[t] = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
-                       ld16<V8>(&DS[(qt * 32 + col) * KTS + 16 * j + 8 * h]), dq[t]);
+                       ld_tr2<V8>(&DSt[(16 * j + tr_key) * QS2 + qt * 32 + tr_q],
+                                  &DSt[(16 * j + 4 + tr_key) * QS2 + qt * 32 + tr_q]),
+                       dq[t]);
     }
     // dq[t][v] is feature 32dt + 8(v/4) + 4h + v%4 of query 32qt + col.
     if constexpr (sizeof(A) == 2) {
