@@ -258,22 +258,24 @@ attend_mfma_kernel(AttnArgs a) {
         }
     } else {
       // Same arithmetic as above on the visible keys (so a query's result
-      // never depends on which queries share its group).
+      // never depends on which queries share its group): hidden keys become
+      // -inf once, and exp2 takes them to 0 (the masks are not kept alive
+      // across both loops).
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          m = fmaxf(m, key <= lim ? s[kt][v] : -INFINITY);
+          s[kt][v] = key <= lim ? s[kt][v] : -INFINITY;
+          m = fmaxf(m, s[kt][v]);
         }
       m = fmaxf(m, __shfl_xor(m, 32)) * a.scale_log2;
+      const float mz = m > -INFINITY ? m : 0.f;  // no visible key: every p is 0
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int key = kt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-          const float p =
-              key <= lim ? __builtin_amdgcn_exp2f(fmaf(s[kt][v], a.scale_log2, -m)) : 0.f;
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[kt][v], a.scale_log2, -mz));
           s[kt][v] = p;
           l += p;
         }

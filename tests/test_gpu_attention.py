@@ -157,6 +157,29 @@ def test_backward_within_tolerance(device, shape, h_kv, bs, tk):
         assert mean_abs_error(ours, tr) <= BF16_MEAN_ABS, name
 
 
+@pytest.mark.parametrize("shape,h_kv,bs,tk", [((1, 1024, 4, 64), 2, 64, 3),
+                                             ((1, 1024, 2, 128), 2, 128, 4)])
+def test_backward_fp16_within_tolerance(device, shape, h_kv, bs, tk):
+    """The float16 backward (same kernels, float16 operands and partials)
+    against the float64 oracle, with the oracle's own float16 error as the
+    yardstick."""
+    cfg = MoBAConfig(block_size=bs, top_k=tk)
+    q, k, v = make_qkv(shape, torch.float16, seed=13, device=device)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    g = make_qkv(shape, torch.float16, seed=14, device=device, n=1)[0]
+    sel = oracle_selection(q, k, cfg)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = moba_attention(qq, kk, vv, cfg)
+    out.backward(g)
+    truth = grads_oracle(q, k, v, cfg, sel, g)
+    low = grads_oracle(q, k, v, cfg, sel, g, dtype=torch.float16)
+    for name, ours, ref, tr in [("dq", qq.grad, low[0], truth[0]), ("dk", kk.grad, low[1], truth[1]),
+                                ("dv", vv.grad, low[2], truth[2])]:
+        assert_within_tolerance(ours, tr, max_abs_error(ref, tr), name)
+        assert max_abs_error(ours, tr) <= BF16_MAX_ABS, name
+        assert mean_abs_error(ours, tr) <= BF16_MEAN_ABS, name
+
+
 def test_backward_fp32_matches_autograd(device):
     cfg = MoBAConfig(block_size=64, top_k=4, dtype=torch.float32)
     shape = (1, 512, 2, 64)
