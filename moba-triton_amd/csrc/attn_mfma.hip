@@ -329,7 +329,9 @@ attend_mfma_kernel(AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
         const int64_t rd = __shfl(dst, lane / RQ + (64 / RQ) * u);
-        if (rd >= 0) *reinterpret_cast<u32x4*>(acc_out + rd * D + (lane % RQ) * 8) = ov[u];
+        // Non-temporal: each partial row is read once, by the merge.
+        if (rd >= 0)
+          __builtin_nontemporal_store(ov[u], reinterpret_cast<u32x4*>(acc_out + rd * D + (lane % RQ) * 8));
       }
     } else {
       if (more) stage_q();
