@@ -44,10 +44,15 @@ pool_kernel(const T* __restrict__ k, T* __restrict__ kbar,
   double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (ok && lo < sp.len) {
     const T* src = k + ((sp.bos + lo + ts) * h_kv + h) * D + d0;
+    // Unrolled, so a lane keeps several rows in flight; non-temporal, since
+    // every row of K is read once here.
+#pragma unroll 8
     for (int64_t t = lo + ts; t < hi; t += TS, src += TS * h_kv * D) {
       T x[8];
       if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<uint4*>(x) = *reinterpret_cast<const uint4*>(src);
+        typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<u32x4_nt*>(x) =
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(src));
       } else {
         reinterpret_cast<uint4*>(x)[0] = reinterpret_cast<const uint4*>(src)[0];
         reinterpret_cast<uint4*>(x)[1] = reinterpret_cast<const uint4*>(src)[1];
