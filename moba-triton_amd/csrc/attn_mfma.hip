@@ -739,7 +739,10 @@ bwd_mfma_kernel(AttnArgs a) {
 
 template <typename T, typename A, int D, int BS>
 static int launch_bwd(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
-  constexpr int NQ = D == 128 ? 32 : 64;
+  // 64 queries per step; at head_dim 128 only with 128-key blocks (88 KiB of
+  // LDS, one workgroup per CU as the registers already require), since the
+  // smaller blocks' variants would spill.
+  constexpr int NQ = (D == 128 && BS != 128) ? 32 : 64;
   dim3 grid(static_cast<unsigned>(a.seg ? a.seg_cap : a.n_blocks), static_cast<unsigned>(n_cols));
   hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS, NQ>), grid, dim3(BS * 2), 0, st, a);
   return check_launch("moba_bwd (mfma)");
