@@ -409,7 +409,7 @@ bwd_mfma_kernel(AttnArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec;
   using Sc = typename M::scalar;
-  // NQ: queries per step (64 at head_dim 64; 32 at 128 to fit LDS)
+  // NQ: queries per step (64; 32 at head_dim 128 with blocks under 128 keys)
   constexpr int QT = NQ / 32;   // query tiles of 32
   constexpr int NW = BS / 32;   // waves: 32 keys each
   constexpr int NT = NW * 64;   // threads
