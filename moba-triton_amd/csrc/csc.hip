@@ -114,12 +114,35 @@ tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restri
   __syncthreads();
   // Query i of this thread: t0 + threadIdx.x + kTileT * i (a wave's lanes
   // hold consecutive queries).
-  for (int i = 0; i < kTileQ / kTileT; ++i) {
-    const int64_t t = t0 + threadIdx.x + kTileT * i;
-    const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
-    for (int j = 0; j < slots; ++j) {
-      const int32_t blk = t < sp.len ? block_idx[qid * slots + j] : -1;
-      bin_add(bins, blk, blk >= 0 && blk < nvis);
+  constexpr int QPT = kTileQ / kTileT;
+  if (slots == 8) {
+    // Every id of the thread's queries requested up front (two 16-byte
+    // loads per query), then counted.
+    int4 ids[QPT][2];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int64_t t = t0 + threadIdx.x + kTileT * i;
+      const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
+      const int4* p = reinterpret_cast<const int4*>(block_idx + (t < sp.len ? qid : 0) * 8);
+      ids[i][0] = t < sp.len ? p[0] : int4{-1, -1, -1, -1};
+      ids[i][1] = t < sp.len ? p[1] : int4{-1, -1, -1, -1};
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int32_t v[4] = {ids[i][h].x, ids[i][h].y, ids[i][h].z, ids[i][h].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) bin_add(bins, v[w], v[w] >= 0 && v[w] < nvis);
+      }
+  } else {
+    for (int i = 0; i < QPT; ++i) {
+      const int64_t t = t0 + threadIdx.x + kTileT * i;
+      const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
+      for (int j = 0; j < slots; ++j) {
+        const int32_t blk = t < sp.len ? block_idx[qid * slots + j] : -1;
+        bin_add(bins, blk, blk >= 0 && blk < nvis);
+      }
     }
   }
   __syncthreads();
