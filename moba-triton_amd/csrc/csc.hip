@@ -183,10 +183,12 @@ unit_chunk_kernel(int32_t* __restrict__ table, int32_t* __restrict__ csum,
   int32_t* cs = csum + (rhk * nchunks + c) * n_blocks + b;
   if (kPhase == 0) {
     int32_t acc = 0;
+#pragma unroll 8
     for (int64_t u = u0; u < u1; ++u) acc += table[u * n_blocks + b];
     *cs = acc;
   } else {
     int32_t run = col_offsets[rhk * (n_blocks + 1) + b] + *cs;
+#pragma unroll 8
     for (int64_t u = u0; u < u1; ++u) {
       const int32_t v = table[u * n_blocks + b];
       table[u * n_blocks + b] = run;
@@ -204,6 +206,7 @@ chunk_scan_kernel(int32_t* __restrict__ csum, int32_t* __restrict__ col_nnz, int
   const int64_t rhk = blockIdx.y;
   if (b >= n_blocks) return;
   int32_t run = 0;
+#pragma unroll 8
   for (int64_t c = 0; c < nchunks; ++c) {
     int32_t* p = csum + (rhk * nchunks + c) * n_blocks + b;
     const int32_t v = *p;
