@@ -20,9 +20,9 @@
 // masks, m = max(q.k * D^-1/2 * log2 e), p = exp2(s - m) rounded to the
 // input dtype for the PV product, l = sum p (float32), partials stored at the
 // query's fixed slot.
-#include "attn_common.h"
-
 #include <type_traits>
+
+#include "attn_common.h"
 
 namespace moba {
 
@@ -564,6 +564,13 @@ bwd_mfma_kernel(AttnArgs a) {
       *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = pv[u] ? po[u] : u32x4{0, 0, 0, 0};
     }
     __syncthreads();
+    // Every entry of the step sees the whole block (a strictly past, full
+    // block) or is dead: the causal masks can go. A dead entry's Q and dO
+    // rows are zero, so it adds nothing to dK / dV either way, and its dQ is
+    // never stored. Each wave reads the same NQ limits, so the vote is
+    // uniform over the workgroup.
+    const bool all_visible = __all(lane >= NQ || s_lim[lane < NQ ? lane : 0] == BS - 1 ||
+                                   s_lim[lane < NQ ? lane : 0] < 0);
     const bool more = g0 + NQ < c.n;
     if (more) {
       fetch();
@@ -583,20 +590,25 @@ bwd_mfma_kernel(AttnArgs a) {
         pacc = M::mma(ld16<V8>(oa + 16 * k), vb[k], pacc);
       }
       V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
+      auto softmax = [&](auto masked) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {  // queries 32qt + 8g + 4h + [0, 4)
         const int q0 = qt * 32 + 8 * g + 4 * h;
-        const int4 lim4 = *reinterpret_cast<const int4*>(&s_lim[q0]);
+        int limv[4] = {BS, BS, BS, BS};
+        if constexpr (decltype(masked)::value) {
+          const int4 lim4 = *reinterpret_cast<const int4*>(&s_lim[q0]);
+          limv[0] = lim4.x; limv[1] = lim4.y; limv[2] = lim4.z; limv[3] = lim4.w;
+        }
         const float4 lse4 = *reinterpret_cast<const float4*>(&s_lse[q0]);
         const float4 dl4 = *reinterpret_cast<const float4*>(&s_delta[q0]);
-        const int limv[4] = {lim4.x, lim4.y, lim4.z, lim4.w};
         const float lsev[4] = {lse4.x, lse4.y, lse4.z, lse4.w};
         const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
         float dsf[4];  // this key's dS of the four queries: one 8-byte row piece
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const int v = 4 * g + w;
-          const float x = mykey <= limv[w] ? sacc[v] * a.scale_log2 - lsev[w] : -INFINITY;
+          const float x = (!decltype(masked)::value || mykey <= limv[w])
+                              ? sacc[v] * a.scale_log2 - lsev[w] : -INFINITY;
           const float p = __builtin_amdgcn_exp2f(x);
           const float ds = p * (pacc[v] - dlv[w]);
           pb[v >> 3][v & 7] = static_cast<Sc>(p);
@@ -608,6 +620,9 @@ bwd_mfma_kernel(AttnArgs a) {
         *reinterpret_cast<uint2*>(&DSt[mykey * QS2 + q0]) = __builtin_bit_cast(
             uint2, __builtin_convertvector(f32x4_t{dsf[0], dsf[1], dsf[2], dsf[3]}, sc4_t));
       }
+      };
+      if (all_visible) softmax(std::false_type{});
+      else softmax(std::true_type{});
       // dV^T += dO^T . P and dK^T += Q^T . dS. The A operands are dO / Q
       // read transposed: lane (group g = lane / 16, r = lane % 16) addresses
       // row 32qt + 16j + 8m + 4h + r / 4, features 32dt + 16(g % 2) + 4(r % 4)
