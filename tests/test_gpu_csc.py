@@ -182,19 +182,23 @@ def entries(index, r, kv):
                         index.slot_of_pair[r, kv, :tot].long().cpu()], 1)
 
 
-@pytest.mark.parametrize("s,nb,packed", [(8000, 1000, False), (8000, 1000, True),
-                                         (24000, 12000, False),   # > 64 KiB of LDS
-                                         (40000, 20000, False)])  # atomic fallback
-def test_csc_column_order(device, s, nb, packed):
+@pytest.mark.parametrize("s,nb,packed,slots", [(8000, 1000, False, 4), (8000, 1000, True, 4),
+                                               (8000, 1000, False, 1),   # rows in halves
+                                               (8000, 1000, False, 3),   # queries straddle rows
+                                               (6000, 1000, True, 5),
+                                               (24000, 12000, False, 4),  # > 64 KiB of LDS
+                                               (40000, 20000, False, 4)])  # atomic fallback
+def test_csc_column_order(device, s, nb, packed, slots):
     """Up to 16384 columns the entries of a column come in (query head, row)
     order; past that (atomic cursors) the same entries in some order."""
-    h_q, h_kv, slots = 4, 2, 4
+    h_q, h_kv = 4, 2
     cfg = MoBAConfig(block_size=64, top_k=slots)
-    lens = [3000, 1000, 4000] if packed else None
+    lens = ([3000, 1000, 4000] if s == 8000 else [2500, 1500, 2000]) if packed else None
     rps = max(lens) if packed else s
     bs_eff = -(-rps // nb)
     idx = synthetic_ids(1 if packed else 2, h_q, s, slots, bs_eff, seed=11, lens=lens)
-    cu = torch.tensor([0, 3000, 4000, 8000], dtype=torch.int32) if packed else None
+    cu = (torch.tensor([0] + lens, dtype=torch.int32).cumsum(0).to(torch.int32)
+          if packed else None)
     got = build_csc_from_indices(idx.to(device), nb, cfg, num_kv_heads=h_kv,
                                  cu_seqlens=None if cu is None else cu.to(device),
                                  max_seqlen=rps if packed else None)
