@@ -94,12 +94,14 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * col_nnz [R, Hkv, nb], col_offsets [R, Hkv, nb + 1] (exclusive prefix
  * sum), row_indices / head_indices / slot_of_pair [R, Hkv, cap] with
  * cap = (Hq / Hkv) * rows_per_seq * slots, order [R, Hkv, nb] (column ids by
- * count desc, id asc). Each (query, slot) pair appears exactly once. With
- * nb <= 16384 a column's entries are in (query head, row) order -- the
- * order of the dense-mask builder, routing.py:467-561 -- on every build, so
- * the backward's dK / dV sums are bitwise reproducible; with more blocks
- * they claim positions by atomic cursors and their order inside a column is
- * unspecified (as in the reference's scatter, routing.py:35-52).
+ * count desc, id asc). Each (query, slot) pair appears exactly once. A
+ * column's entries are in (query head, row) order -- the order of the
+ * dense-mask builder, routing.py:467-561 -- on every build, so the
+ * backward's dK / dV sums are bitwise reproducible. Columns are placed in
+ * windows of 16384 (each window re-reads block_idx). Only on a device that
+ * cannot give one workgroup 128 KiB of LDS do entries claim positions by
+ * atomic cursors, their order inside a column then being unspecified (as in
+ * the reference's scatter, routing.py:35-52).
  * row_indices hold packed token indices when cu_seqlens is given.
  * Ids outside [0, n_blocks), and ids past the last block a query of the
  * same 1024-query tile can see, are ignored like the -1 padding (moba_gate
@@ -122,9 +124,10 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
  * routing.py:73-130.
  */
 /* Workspace of moba_csc_build in bytes; rows_per_seq is seq_len, or
- * max_seqlen when packed. For nb <= 16384 it holds a count table of
- * R * Hq * ceil(rows_per_seq / 1024) * nb int32 plus chunk sums of
- * R * Hkv * nb * (at most 64) int32; past that R * Hkv * nb int32 cursors. */
+ * max_seqlen when packed. With W = min(nb, 16384) it holds a count table of
+ * R * Hq * ceil(rows_per_seq / 1024) * W int32 plus chunk sums of
+ * R * Hkv * W * (at most 64) int32 (never less than R * Hkv * nb int32, the
+ * atomic cursors of the fallback). */
 size_t moba_csc_workspace_size(int64_t batch, int64_t rows_per_seq, int64_t h_q,
                                int64_t h_kv, int64_t n_blocks,
                                int64_t slots);

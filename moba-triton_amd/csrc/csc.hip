@@ -5,10 +5,13 @@
 // block), an exclusive scan into col_offsets, a longest-first column order
 // (count desc, id asc; the stable argsort of routing.py:548-553), and a
 // scatter of (row, query head, slot) triples. Under GQA every query head of
-// a group lands in its kv head's columns. Up to kDetMaxCols (16384) columns
-// the scatter places a column's entries in (query head, row) order on every
-// build; past that it falls back to per-entry atomic cursors, whose order
-// within a column varies from run to run, as the reference's does.
+// a group lands in its kv head's columns. The scatter places a column's
+// entries in (query head, row) order on every build. It works on windows of
+// up to kDetMaxCols (16384) columns, the (cursor, mask) pairs of one window
+// filling 128 KiB of LDS: past that many columns the windows run one after
+// another, each reading every id again. Only a device that cannot give a
+// workgroup that much LDS falls back to per-entry atomic cursors, whose
+// order within a column varies from run to run, as the reference's does.
 //
 // The order pass ranks each column directly -- rank = #columns with a larger
 // count, or the same count and a smaller id -- one lane per column against an
@@ -73,6 +76,14 @@ typedef int32_t i32x3 __attribute__((ext_vector_type(3), aligned(4)));
 constexpr int kTileT = 256;
 constexpr int kMaxBins = 16384;
 
+// Columns of the window [lo, lo + width) that queries seeing `nv` blocks can
+// hold: [lo, lo + result).
+__device__ inline int window_visible(int64_t nv, int64_t n_blocks, int64_t lo, int64_t width) {
+  const int64_t hi = nv < n_blocks ? nv : n_blocks;
+  const int64_t n = hi - lo;
+  return static_cast<int>(n < 0 ? 0 : (n > width ? width : n));
+}
+
 // atomicAdd(&bins[blk], 1) for every active lane, with the lanes that share
 // the first active lane's id served by one atomic (every query of a block
 // selects its own block, so a wave's 64 consecutive queries usually agree
@@ -89,27 +100,26 @@ __device__ inline void bin_add(int32_t* bins, int32_t blk, bool active) {
   if (active && !same) atomicAdd(&bins[blk], 1);
 }
 
-// table row (rh * tiles + tile) = the tile's count of every column, zeros
-// where it sees none; grid (tiles, R * Hq).
+// table row (rh * tiles + tile) = the tile's count of every column of the
+// window [lo, lo + width), zeros where it sees none; grid (tiles, R * Hq).
 __global__ void __launch_bounds__(kTileT)
 tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restrict__ cu,
                   int64_t S, int64_t h_q, int64_t n_blocks, int64_t bs, int slots,
-                  int32_t* __restrict__ table) {
-  extern __shared__ int32_t bins[];  // nb counters (dynamic LDS)
+                  int32_t* __restrict__ table, int64_t lo, int64_t width) {
+  extern __shared__ int32_t bins[];  // width counters (dynamic LDS)
   const int64_t rh = blockIdx.y;
   const int64_t r = rh / h_q;
   const int64_t hq = rh % h_q;
   const bool packed = cu != nullptr;
   const SeqSpan sp = seq_span(cu, r, S);
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTileQ;
-  int32_t* trow = table + (rh * gridDim.x + blockIdx.x) * n_blocks;
+  int32_t* trow = table + (rh * gridDim.x + blockIdx.x) * width;
   if (t0 >= sp.len) {
-    for (int64_t b = threadIdx.x; b < n_blocks; b += kTileT) trow[b] = 0;
+    for (int64_t b = threadIdx.x; b < width; b += kTileT) trow[b] = 0;
     return;
   }
   const int64_t t_last = (t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len) - 1;
-  const int64_t nv = t_last / bs + 1;  // blocks any query here can select
-  const int nvis = static_cast<int>(nv < n_blocks ? nv : n_blocks);
+  const int nvis = window_visible(t_last / bs + 1, n_blocks, lo, width);
   for (int b = threadIdx.x; b < nvis; b += kTileT) bins[b] = 0;
   __syncthreads();
   // Query i of this thread: t0 + threadIdx.x + kTileT * i (a wave's lanes
@@ -133,20 +143,23 @@ tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restri
       for (int h = 0; h < 2; ++h) {
         const int32_t v[4] = {ids[i][h].x, ids[i][h].y, ids[i][h].z, ids[i][h].w};
 #pragma unroll
-        for (int w = 0; w < 4; ++w) bin_add(bins, v[w], v[w] >= 0 && v[w] < nvis);
+        for (int w = 0; w < 4; ++w) {
+          const int32_t c = v[w] - static_cast<int32_t>(lo);
+          bin_add(bins, c, c >= 0 && c < nvis);
+        }
       }
   } else {
     for (int i = 0; i < QPT; ++i) {
       const int64_t t = t0 + threadIdx.x + kTileT * i;
       const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
       for (int j = 0; j < slots; ++j) {
-        const int32_t blk = t < sp.len ? block_idx[qid * slots + j] : -1;
-        bin_add(bins, blk, blk >= 0 && blk < nvis);
+        const int32_t c = t < sp.len ? block_idx[qid * slots + j] - static_cast<int32_t>(lo) : -1;
+        bin_add(bins, c, c >= 0 && c < nvis);
       }
     }
   }
   __syncthreads();
-  for (int64_t b = threadIdx.x; b < n_blocks; b += kTileT) trow[b] = b < nvis ? bins[b] : 0;
+  for (int64_t b = threadIdx.x; b < width; b += kTileT) trow[b] = b < nvis ? bins[b] : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -172,48 +185,49 @@ template <int kPhase>
 __global__ void __launch_bounds__(256)
 unit_chunk_kernel(int32_t* __restrict__ table, int32_t* __restrict__ csum,
                   const int32_t* __restrict__ col_offsets, int64_t n_blocks, int64_t h_q,
-                  int64_t h_kv, int64_t units, int64_t chunk, int64_t nchunks) {
+                  int64_t h_kv, int64_t units, int64_t chunk, int64_t nchunks, int64_t lo,
+                  int64_t width) {
   const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t c = blockIdx.y;
   const int64_t rhk = blockIdx.z;
-  if (b >= n_blocks) return;
+  if (b >= width) return;
   const int64_t r = rhk / h_kv, hk = rhk % h_kv;
   const int64_t u0 = (r * h_q + hk * (h_q / h_kv)) * (units / (h_q / h_kv)) + c * chunk;
   const int64_t u1 = c * chunk + chunk < units ? u0 + chunk : u0 + (units - c * chunk);
-  int32_t* cs = csum + (rhk * nchunks + c) * n_blocks + b;
+  int32_t* cs = csum + (rhk * nchunks + c) * width + b;
   if (kPhase == 0) {
     int32_t acc = 0;
 #pragma unroll 8
-    for (int64_t u = u0; u < u1; ++u) acc += table[u * n_blocks + b];
+    for (int64_t u = u0; u < u1; ++u) acc += table[u * width + b];
     *cs = acc;
   } else {
-    int32_t run = col_offsets[rhk * (n_blocks + 1) + b] + *cs;
+    int32_t run = col_offsets[rhk * (n_blocks + 1) + lo + b] + *cs;
 #pragma unroll 8
     for (int64_t u = u0; u < u1; ++u) {
-      const int32_t v = table[u * n_blocks + b];
-      table[u * n_blocks + b] = run;
+      const int32_t v = table[u * width + b];
+      table[u * width + b] = run;
       run += v;
     }
   }
 }
 
 // csum[rhk, :, b] -> exclusive scan over the chunks; the total is the
-// column's count.
+// column's count (written to col_nnz unless that is null).
 __global__ void __launch_bounds__(256)
 chunk_scan_kernel(int32_t* __restrict__ csum, int32_t* __restrict__ col_nnz, int64_t n_blocks,
-                  int64_t nchunks) {
+                  int64_t nchunks, int64_t width) {
   const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t rhk = blockIdx.y;
-  if (b >= n_blocks) return;
+  if (b >= width) return;
   int32_t run = 0;
 #pragma unroll 8
   for (int64_t c = 0; c < nchunks; ++c) {
-    int32_t* p = csum + (rhk * nchunks + c) * n_blocks + b;
+    int32_t* p = csum + (rhk * nchunks + c) * width + b;
     const int32_t v = *p;
     *p = run;
     run += v;
   }
-  col_nnz[rhk * n_blocks + b] = run;
+  if (col_nnz) col_nnz[rhk * n_blocks + b] = run;
 }
 
 // One wave per unit. Its entries (query t, slot j) are contiguous in
@@ -234,7 +248,8 @@ chunk_scan_kernel(int32_t* __restrict__ csum, int32_t* __restrict__ col_nnz, int
 // Ids are prefetched a stage of kPer rows ahead into registers: a wave's
 // global stores share its load counter, so a load waited on between the
 // stores would also wait for every store before it.
-// Dynamic LDS: (cursor, mask) pairs of nb columns.
+// Only columns of the window [lo, lo + width) are placed (the table holds
+// that window). Dynamic LDS: (cursor, mask) pairs of the window's columns.
 constexpr int kPer = 16;
 // Columns the deterministic build handles (8 bytes of LDS each).
 constexpr int kDetMaxCols = kMaxBins;
@@ -244,8 +259,9 @@ det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restr
                    int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int64_t bs,
                    int slots, int64_t cap, const int32_t* __restrict__ table,
                    int32_t* __restrict__ row_indices, int32_t* __restrict__ head_indices,
-                   int32_t* __restrict__ slot_of_pair, int64_t istride, bool records) {
-  extern __shared__ uint32_t cm[];  // (cursor, mask) per column
+                   int32_t* __restrict__ slot_of_pair, int64_t istride, bool records,
+                   int64_t lo, int64_t width) {
+  extern __shared__ uint32_t cm[];  // (cursor, mask) per column of the window
   const int64_t tile = blockIdx.x;
   const int64_t rh = blockIdx.y;
   const int64_t unit = rh * gridDim.x + tile;
@@ -257,9 +273,9 @@ det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restr
   const int64_t t0 = tile * kTileQ;
   if (t0 >= sp.len) return;
   const int64_t t1 = t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len;
-  const int64_t nv = (t1 - 1) / bs + 1;
-  const int nvis = static_cast<int>(nv < n_blocks ? nv : n_blocks);
-  const int32_t* trow = table + unit * n_blocks;
+  const int nvis = window_visible((t1 - 1) / bs + 1, n_blocks, lo, width);
+  if (nvis == 0) return;  // no column of the window is visible here
+  const int32_t* trow = table + unit * width;
   const int lane = threadIdx.x;
   for (int b0 = 0; b0 < nvis; b0 += 16 * 64) {  // 16 loads in flight per lane
     int32_t v[16];
@@ -304,7 +320,7 @@ det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restr
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       if (s0 + u * 64 < n_ent) {
-        const int32_t blk = cur[u];
+        const int32_t blk = cur[u] - static_cast<int32_t>(lo);  // window column
         const bool valid = blk >= 0 && blk < nvis;
         for (int h = 0; h < halves; ++h) {
           const bool ok = valid && (halves == 1 || (lane >> 5) == h);
@@ -528,11 +544,15 @@ bool det_lds_ok(size_t bytes) {
 extern "C" size_t moba_csc_workspace_size(int64_t batch, int64_t rows_per_seq, int64_t h_q,
                                           int64_t h_kv, int64_t n_blocks, int64_t slots) {
   (void)slots;
-  if (n_blocks > moba::kDetMaxCols)  // atomic cursors of the untiled build
-    return sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n_blocks);
+  // Unit table and chunk sums of one column window. This is never smaller
+  // than the atomic cursors of the untiled build (batch * h_kv * n_blocks),
+  // which run in the same memory when the device lacks the LDS.
   const UnitPlan p = unit_plan(rows_per_seq, h_q, h_kv);
-  return sizeof(int32_t) * static_cast<size_t>(batch * n_blocks *
-                                               (h_q * p.tiles + h_kv * p.nchunks));
+  const int64_t width = n_blocks < moba::kDetMaxCols ? n_blocks : moba::kDetMaxCols;
+  const size_t det = sizeof(int32_t) * static_cast<size_t>(batch * width *
+                                                          (h_q * p.tiles + h_kv * p.nchunks));
+  const size_t cur = sizeof(int32_t) * static_cast<size_t>(batch * h_kv * n_blocks);
+  return det > cur ? det : cur;
 }
 
 extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
@@ -573,32 +593,53 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   const unsigned fill_blocks = static_cast<unsigned>(cdiv(ncols, 256) < 4096 ? cdiv(ncols, 256) : 4096);
   // A lower bound on the block size: cdiv(rows, n_blocks) <= block_size, so
   // t / bs_eff never under-counts the blocks a query can see.
-  const size_t det_lds = 8 * static_cast<size_t>(n_blocks);
-  const bool tiled = n_blocks <= kDetMaxCols && det_lds_ok(det_lds);
+  // Columns go in windows of at most kDetMaxCols (the LDS of one scatter).
+  const int64_t win = n_blocks < kDetMaxCols ? n_blocks : kDetMaxCols;
+  const int64_t n_win = cdiv(n_blocks, win);
+  const size_t det_lds = 8 * static_cast<size_t>(win);
+  const bool tiled = det_lds_ok(det_lds);
   const int64_t bs_eff = cdiv(g.rows_per_seq, n_blocks);
   const UnitPlan up = unit_plan(g.rows_per_seq, h_q, h_kv);
-  const unsigned col_groups = static_cast<unsigned>(cdiv(n_blocks, 256));
   const unsigned rhk = static_cast<unsigned>(batch * h_kv);
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq * slots, 256)),
             static_cast<unsigned>(batch * h_q));
   dim3 tgrid(static_cast<unsigned>(up.tiles), static_cast<unsigned>(batch * h_q));
   int32_t* table = static_cast<int32_t*>(workspace);
-  int32_t* csum = table + batch * h_q * up.tiles * n_blocks;
+  int32_t* csum = table + batch * h_q * up.tiles * win;
   int32_t* cursor = static_cast<int32_t*>(workspace);
-  if (tiled) {
-    // Deterministic build: per-unit counts, scanned into per-unit bases.
+  // Deterministic build of the window [lo, lo + width): per-unit counts,
+  // scanned into per-unit bases (after col_offsets exist), then placed.
+  auto window_counts = [&](int64_t lo, int64_t width, int32_t* nnz) {
     hipLaunchKernelGGL(tile_count_kernel, tgrid, dim3(kTileT),
-                       static_cast<unsigned>(sizeof(int32_t) * n_blocks), s, block_idx, cu_seqlens,
-                       seq_len, h_q, n_blocks, bs_eff, static_cast<int>(slots), table);
+                       static_cast<unsigned>(sizeof(int32_t) * width), s, block_idx, cu_seqlens,
+                       seq_len, h_q, n_blocks, bs_eff, static_cast<int>(slots), table, lo,
+                       width);
     hipLaunchKernelGGL(unit_chunk_kernel<0>,
-                       dim3(col_groups, static_cast<unsigned>(up.nchunks), rhk), dim3(256), 0,
-                       s, table, csum, nullptr, n_blocks, h_q, h_kv, up.units, up.chunk,
-                       up.nchunks);
-    hipLaunchKernelGGL(chunk_scan_kernel, dim3(col_groups, rhk), dim3(256), 0, s, csum,
-                       col_nnz, n_blocks, up.nchunks);
+                       dim3(static_cast<unsigned>(cdiv(width, 256)),
+                            static_cast<unsigned>(up.nchunks), rhk),
+                       dim3(256), 0, s, table, csum, nullptr, n_blocks, h_q, h_kv, up.units,
+                       up.chunk, up.nchunks, lo, width);
+    hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>(cdiv(width, 256)), rhk),
+                       dim3(256), 0, s, csum, nnz, n_blocks, up.nchunks, width);
+  };
+  auto window_place = [&](int64_t lo, int64_t width) {
+    hipLaunchKernelGGL(unit_chunk_kernel<1>,
+                       dim3(static_cast<unsigned>(cdiv(width, 256)),
+                            static_cast<unsigned>(up.nchunks), rhk),
+                       dim3(256), 0, s, table, csum, col_offsets, n_blocks, h_q, h_kv,
+                       up.units, up.chunk, up.nchunks, lo, width);
+    hipLaunchKernelGGL(det_scatter_kernel, tgrid, dim3(64),
+                       static_cast<unsigned>(8 * width), s, block_idx, cu_seqlens, seq_len, h_q,
+                       h_kv, n_blocks, bs_eff, static_cast<int>(slots), cap, table, row_indices,
+                       head_indices, slot_of_pair, index_stride, records, lo, width);
+  };
+  if (tiled && n_win == 1) {
+    window_counts(0, n_blocks, col_nnz);
   } else {
+    // Column counts by atomics (their sums do not depend on the order).
     hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, col_nnz, ncols, 0);
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, cursor, ncols, 0);
+    if (!tiled)
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_blocks), dim3(256), 0, s, cursor, ncols, 0);
     hipLaunchKernelGGL(count_or_scatter_kernel<false>, grid, dim3(256), 0, s, block_idx,
                        cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,
                        static_cast<int>(slots), cap, col_nnz, nullptr, nullptr, nullptr,
@@ -611,15 +652,17 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
     hipLaunchKernelGGL(seg_build_kernel, dim3(rhk), dim3(1024), 0, s, col_nnz, order, n_blocks,
                        seg_len, static_cast<int>(max_seg), segments, seg_split, seg_counts,
                        seg_cap);
-  if (tiled) {
-    hipLaunchKernelGGL(unit_chunk_kernel<1>,
-                       dim3(col_groups, static_cast<unsigned>(up.nchunks), rhk), dim3(256), 0,
-                       s, table, csum, col_offsets, n_blocks, h_q, h_kv, up.units, up.chunk,
-                       up.nchunks);
-    hipLaunchKernelGGL(det_scatter_kernel, tgrid, dim3(64),
-                       static_cast<unsigned>(det_lds), s, block_idx, cu_seqlens, seq_len, h_q, h_kv, n_blocks, bs_eff,
-                       static_cast<int>(slots), cap, table, row_indices, head_indices,
-                       slot_of_pair, index_stride, records);
+  if (tiled && n_win == 1) {
+    window_place(0, n_blocks);
+  } else if (tiled) {
+    // One window after another through the same table; the counts again,
+    // now per unit (col_nnz already holds their totals).
+    for (int64_t w = 0; w < n_win; ++w) {
+      const int64_t lo = w * win;
+      const int64_t width = n_blocks - lo < win ? n_blocks - lo : win;
+      window_counts(lo, width, nullptr);
+      window_place(lo, width);
+    }
   } else {
     hipLaunchKernelGGL(count_or_scatter_kernel<true>, grid, dim3(256), 0, s, block_idx,
                        cu_seqlens, seq_len, g.rows_per_seq, h_q, h_kv, n_blocks,

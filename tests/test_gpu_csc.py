@@ -187,13 +187,15 @@ def entries(index, r, kv):
                                                (8000, 1000, False, 3),   # queries straddle rows
                                                (6000, 1000, True, 5),
                                                (24000, 12000, False, 4),  # > 64 KiB of LDS
-                                               (40000, 20000, False, 4)])  # atomic fallback
+                                               (40000, 20000, False, 4),  # two windows
+                                               (60000, 40000, True, 3)])  # three windows
 def test_csc_column_order(device, s, nb, packed, slots):
-    """Up to 16384 columns the entries of a column come in (query head, row)
-    order; past that (atomic cursors) the same entries in some order."""
+    """The entries of a column come in (query head, row) order, also past
+    16384 columns, where the build places the columns window by window."""
     h_q, h_kv = 4, 2
     cfg = MoBAConfig(block_size=64, top_k=slots)
-    lens = ([3000, 1000, 4000] if s == 8000 else [2500, 1500, 2000]) if packed else None
+    lens = {8000: [3000, 1000, 4000], 6000: [2500, 1500, 2000],
+            60000: [15000, 5000, 40000]}[s] if packed else None
     rps = max(lens) if packed else s
     bs_eff = -(-rps // nb)
     idx = synthetic_ids(1 if packed else 2, h_q, s, slots, bs_eff, seed=11, lens=lens)
@@ -204,12 +206,7 @@ def test_csc_column_order(device, s, nb, packed, slots):
                                  max_seqlen=rps if packed else None)
     want = canonical(idx, nb, h_kv, cu)
     for (r, kv), w in want.items():
-        e = entries(got, r, kv)
-        if nb <= 16384:
-            assert torch.equal(e, w), (r, kv)
-        else:
-            k = lambda x: (x[:, 0] * h_q + x[:, 1]) * (1 << 40) + x[:, 2]
-            assert torch.equal(e[k(e).argsort()], w), (r, kv)
+        assert torch.equal(entries(got, r, kv), w), (r, kv)
 
 
 def test_gradients_are_bitwise_stable_across_index_builds(device):

@@ -59,5 +59,8 @@ def test_workspace_queries_are_host_only():
     # count table: 4 heads x 64 tiles x 512 columns; chunk sums: 4 kv heads x
     # 4 chunks (64 units in chunks of 16) x 512 columns
     assert lib.moba_csc_workspace_size(1, 65536, 4, 4, 512, 8) == 4 * (4 * 64 + 4 * 4) * 512
-    # past 16384 columns: one atomic cursor per column
-    assert lib.moba_csc_workspace_size(2, 1 << 22, 4, 2, 32768, 8) == 4 * 2 * 2 * 32768
+    # past 16384 columns: the table of one 16384-column window
+    tiles = (1 << 22) // 1024
+    chunk = -(-2 * tiles // 64)
+    assert lib.moba_csc_workspace_size(2, 1 << 22, 4, 2, 32768, 8) == \
+        4 * 2 * 16384 * (4 * tiles + 2 * (-(-2 * tiles // chunk)))
