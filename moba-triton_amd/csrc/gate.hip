@@ -616,9 +616,25 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     // ballot); otherwise each score is written at the lane's next free entry
     // and only a score that beats the threshold advances it (no per-score
     // branch). The fold below keeps 16 free entries for every chunk.
+    // The four compares go straight to wave masks; a lane almost never
+    // holds two scores of one group above its threshold, so when no lane
+    // does (scalar test on the masks) each lane appends its one hit, if
+    // any, as a single entry.
     auto append4 = [&](const float (&x)[4], uint32_t id0) {
-      const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      if (__ballot(mx > thr) != 0) {
+      const bool h0 = x[0] > thr, h1 = x[1] > thr, h2 = x[2] > thr, h3 = x[3] > thr;
+      const uint64_t b0 = __ballot(h0), b1 = __ballot(h1), b2 = __ballot(h2), b3 = __ballot(h3);
+      if ((b0 | b1 | b2 | b3) == 0) return;
+      if (((b0 & (b1 | b2 | b3)) | (b1 & (b2 | b3)) | (b2 & b3)) == 0) {
+        float v = h1 ? x[1] : x[0];
+        v = h2 ? x[2] : v;
+        v = h3 ? x[3] : v;
+        uint32_t w = h1 ? 1u : 0u;
+        w = h2 ? 2u : w;
+        w = h3 ? 3u : w;
+        sv[cnt * 64] = v;
+        si[cnt * 64] = static_cast<uint16_t>(id0 + w);
+        cnt += (h0 || h1 || h2 || h3) ? 1 : 0;
+      } else {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           sv[cnt * 64] = x[w];
