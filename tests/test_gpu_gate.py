@@ -127,3 +127,21 @@ def test_gate_integer_inputs_with_many_exact_ties(device, d, bs, tk):
     q = torch.randint(-2, 3, (1, 8192, 2, d), generator=g).to(torch.bfloat16).to(device)
     k = torch.randint(-1, 2, (1, 8192, 2, d), generator=g).to(torch.bfloat16).to(device)
     check(q, k, cfg)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_gate_every_score_a_candidate(device, d):
+    """Scores rising block by block ((j + 1) / 64 per feature of block j,
+    all-ones queries): with two 32-block chunks pass 1 finds fewer than
+    `take` chunk maxima, so the threshold stays at -inf, every score of pass
+    2 is a candidate and every group appends all four scores; the per-lane
+    buffer must be folded often enough that no candidate is lost."""
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    S = 8192
+    j = torch.arange(S) // 128
+    k = ((j + 1).float() / 64).view(1, S, 1, 1).expand(1, S, 1, d) / (d // 8)
+    k = k.to(torch.bfloat16).contiguous().to(device)
+    q = torch.ones(1, S, 1, d, dtype=torch.bfloat16, device=device)
+    idx = check(q, k, cfg)
+    last = idx[0, 0, -1].tolist()  # the last query: own block 63, top 7 of 0..62
+    assert last == list(range(56, 64)), last
