@@ -9,8 +9,13 @@ the unchanged pipeline (pool, gate, CSC, attend, merge; backward likewise)
 with buffers sized for the chunk, reused from one chunk to the next. Results
 are those of the unchunked run: every stage works per (row, kv head).
 
-A single (row, kv head) unit is never split (that would need query chunks),
-so the smallest chunk's buffers are one unit's.
+A unit whose buffers alone exceed the budget is split further by query head:
+a subset of a kv head's query heads is itself a GQA problem over that kv
+head. The forward and dQ are those of the unchunked run (every (query, slot)
+entry is computed on its own); dK and dV of the kv head are the sum of the
+subsets' contributions, added in float32, so they agree with the one-pass
+result within rounding rather than bit for bit. The smallest chunk is one
+query head of one row.
 """
 
 import os
@@ -38,15 +43,29 @@ def unit_bytes(rows_per_seq: int, group: int, head_dim: int, slots: int, elem: i
     return rows_per_seq * group * slots * (head_dim * elem + 8)
 
 
-def plan_chunks(batch: int, h_kv: int, unit: int, budget: int) -> list[tuple[int, int, int, int]]:
-    """Chunks (b0, b1, hk0, hk1) covering every (batch row, kv head) once:
-    whole batch rows when a row's heads fit together, else head groups of
-    one row; each chunk within `budget` unless a single unit exceeds it."""
+def plan_chunks(batch: int, h_kv: int, unit: int, budget: int,
+                group: int = 1) -> list[tuple[int, int, int, int, int, int]]:
+    """Chunks (b0, b1, hk0, hk1, j0, j1) covering every (batch row, query
+    head) once: rows b0..b1, kv heads hk0..hk1 and, of each kv head's `group`
+    query heads, those j0..j1 (all of them unless the chunk holds a single
+    kv head). Whole batch rows when a row's heads fit together, else kv-head
+    groups of one row, else query-head subsets of one unit; each chunk within
+    `budget` unless a single query head of one row exceeds it."""
     if batch * h_kv * unit <= budget:
-        return [(0, batch, 0, h_kv)]
+        return [(0, batch, 0, h_kv, 0, group)]
     if h_kv * unit <= budget:
         rows = max(1, budget // (h_kv * unit))
-        return [(b0, min(batch, b0 + rows), 0, h_kv) for b0 in range(0, batch, rows)]
-    heads = max(1, budget // unit)
-    return [(b, b + 1, h0, min(h_kv, h0 + heads))
-            for b in range(batch) for h0 in range(0, h_kv, heads)]
+        return [(b0, min(batch, b0 + rows), 0, h_kv, 0, group) for b0 in range(0, batch, rows)]
+    if unit <= budget or group == 1:
+        heads = max(1, budget // unit)
+        return [(b, b + 1, h0, min(h_kv, h0 + heads), 0, group)
+                for b in range(batch) for h0 in range(0, h_kv, heads)]
+    per = max(1, budget // (unit // group))  # query heads of one unit per chunk
+    return [(b, b + 1, hk, hk + 1, j0, min(group, j0 + per))
+            for b in range(batch) for hk in range(h_kv) for j0 in range(0, group, per)]
+
+
+def query_heads(chunk, group: int) -> tuple[int, int]:
+    """First and past-the-last query head of a chunk."""
+    _, _, hk0, hk1, j0, j1 = chunk
+    return hk0 * group + j0, (hk1 - 1) * group + j1

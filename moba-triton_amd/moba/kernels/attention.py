@@ -9,7 +9,7 @@ receives no gradient (`attention.py:33-38`): routing is a hard top-k.
 import torch
 
 from moba import _lib
-from moba.chunking import partials_budget, plan_chunks, unit_bytes
+from moba.chunking import partials_budget, plan_chunks, query_heads, unit_bytes
 from moba.config import MoBAConfig
 from moba.kernels.moba_bwd import moba_backward
 from moba.kernels.moba_fwd import _validate, attend_partials, combine_partials
@@ -22,15 +22,16 @@ def _piece(t, b0, b1, h0, h1):
 
 
 def forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen):
-    """The chunks (b0, b1, hk0, hk1) of (batch row, kv head) units the
-    per-slot buffers of this call are split into (one chunk when they fit
-    the budget of `moba.chunking`)."""
+    """The chunks (b0, b1, hk0, hk1, j0, j1) -- batch rows, kv heads, and
+    query heads within each kv head's group -- the per-slot buffers of this
+    call are split into (one chunk when they fit the budget of
+    `moba.chunking`)."""
     _lib.require_gpu(q, k, v)  # raises before any device query on host tensors
     b, s, h_q, d = q.shape
     h_kv = k.shape[2]
     rps = max_seqlen if cu_seqlens is not None else s
     unit = unit_bytes(rps, h_q // h_kv, d, cfg.slots(), q.element_size())
-    return plan_chunks(b, h_kv, unit, partials_budget(q.device))
+    return plan_chunks(b, h_kv, unit, partials_budget(q.device), group=h_q // h_kv)
 
 
 class MoBAAttentionFunction(torch.autograd.Function):
@@ -38,7 +39,8 @@ class MoBAAttentionFunction(torch.autograd.Function):
 
     Without a caller's index, a call whose per-slot buffers exceed the
     budget of `moba.chunking` runs chunk by chunk over (batch row, kv head)
-    units, forward and backward, with the same results.
+    units, forward and backward, with the same results; a unit too large on
+    its own is split by query head (dK / dV then summed in float32).
     """
 
     @staticmethod
@@ -47,14 +49,16 @@ class MoBAAttentionFunction(torch.autograd.Function):
             cu_seqlens, max_seqlen = index.cu_seqlens, index.max_seqlen
         _validate(q, k, v, cfg, cu_seqlens, max_seqlen)
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        chunks = [(0, q.shape[0], 0, k.shape[2])] if index is not None else \
-            forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen)
         group = q.shape[2] // k.shape[2]
+        chunks = [(0, q.shape[0], 0, k.shape[2], 0, group)] if index is not None else \
+            forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen)
         out = torch.empty_like(q) if len(chunks) > 1 else None
         saved = []
-        for b0, b1, hk0, hk1 in chunks:
+        for chunk in chunks:
+            b0, b1, hk0, hk1 = chunk[:4]
+            hq0, hq1 = query_heads(chunk, group)
             whole = len(chunks) == 1
-            qc = q if whole else _piece(q, b0, b1, hk0 * group, hk1 * group)
+            qc = q if whole else _piece(q, b0, b1, hq0, hq1)
             kc = k if whole else _piece(k, b0, b1, hk0, hk1)
             vc = v if whole else _piece(v, b0, b1, hk0, hk1)
             idx = index if index is not None else build_csc_fused(
@@ -65,7 +69,7 @@ class MoBAAttentionFunction(torch.autograd.Function):
             if whole:
                 out = oc
             else:
-                out[b0:b1, :, hk0 * group:hk1 * group] = oc
+                out[b0:b1, :, hq0:hq1] = oc
             saved.append((idx, lse, part_m))
         ctx.save_for_backward(q, k, v, out)
         ctx.cfg, ctx.causal, ctx.chunks, ctx.saved = cfg, causal, chunks, saved
@@ -81,16 +85,28 @@ class MoBAAttentionFunction(torch.autograd.Function):
             dq, dk, dv = moba_backward(dout, q, k, v, out, lse, part_m, ctx.cfg, idx,
                                        causal=ctx.causal)
             return dq, dk, dv, None, None, None, None, None
-        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        for (b0, b1, hk0, hk1), (idx, lse, part_m) in zip(chunks, ctx.saved):
-            hq0, hq1 = hk0 * group, hk1 * group
+        # Chunks holding part of a kv head's group add into float32 dK / dV.
+        split = any((c[4], c[5]) != (0, group) for c in chunks)
+        dq = torch.empty_like(q)
+        dk, dv = ((torch.zeros(k.shape, dtype=torch.float32, device=k.device),
+                   torch.zeros(v.shape, dtype=torch.float32, device=v.device)) if split
+                  else (torch.empty_like(k), torch.empty_like(v)))
+        for chunk, (idx, lse, part_m) in zip(chunks, ctx.saved):
+            b0, b1, hk0, hk1 = chunk[:4]
+            hq0, hq1 = query_heads(chunk, group)
             g = moba_backward(_piece(dout, b0, b1, hq0, hq1), _piece(q, b0, b1, hq0, hq1),
                               _piece(k, b0, b1, hk0, hk1), _piece(v, b0, b1, hk0, hk1),
                               _piece(out, b0, b1, hq0, hq1), lse, part_m, ctx.cfg, idx,
                               causal=ctx.causal)
             dq[b0:b1, :, hq0:hq1] = g[0]
-            dk[b0:b1, :, hk0:hk1] = g[1]
-            dv[b0:b1, :, hk0:hk1] = g[2]
+            if split:
+                dk[b0:b1, :, hk0:hk1] += g[1].float()
+                dv[b0:b1, :, hk0:hk1] += g[2].float()
+            else:
+                dk[b0:b1, :, hk0:hk1] = g[1]
+                dv[b0:b1, :, hk0:hk1] = g[2]
+        if split:
+            dk, dv = dk.to(k.dtype), dv.to(v.dtype)
         return dq, dk, dv, None, None, None, None, None
 
 

@@ -172,14 +172,17 @@ def moba_forward(q, k, v, cfg: MoBAConfig, index: CSCIndex | None = None,
                                                    partials_dtype=partials_dtype)
         return combine_partials(part_m, part_l, part_acc, q.dtype)
     # Without a caller's index the per-slot buffers are bounded by running
-    # (batch row, kv head) chunks (moba.chunking).
+    # (batch row, kv head[, query heads]) chunks (moba.chunking).
+    from moba.chunking import query_heads
     from moba.kernels.attention import _piece, forward_chunks
     chunks = forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen)
     group = q.shape[2] // k.shape[2]
     out = torch.empty_like(q) if len(chunks) > 1 else None
-    for b0, b1, hk0, hk1 in chunks:
+    for chunk in chunks:
+        b0, b1, hk0, hk1 = chunk[:4]
+        hq0, hq1 = query_heads(chunk, group)
         whole = len(chunks) == 1
-        qc = q if whole else _piece(q, b0, b1, hk0 * group, hk1 * group)
+        qc = q if whole else _piece(q, b0, b1, hq0, hq1)
         kc = k if whole else _piece(k, b0, b1, hk0, hk1)
         vc = v if whole else _piece(v, b0, b1, hk0, hk1)
         idx = build_csc_fused(qc, kc, cfg, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
@@ -188,5 +191,5 @@ def moba_forward(q, k, v, cfg: MoBAConfig, index: CSCIndex | None = None,
         oc = combine_partials(part_m, part_l, part_acc, q.dtype)
         if whole:
             return oc
-        out[b0:b1, :, hk0 * group:hk1 * group] = oc
+        out[b0:b1, :, hq0:hq1] = oc
     return out

@@ -128,20 +128,26 @@ def test_index_stride_layouts():
     assert index_stride(make(*even)) == 2
 
 
-@pytest.mark.parametrize("batch,h_kv,budget_units", [(1, 4, 100), (2, 4, 8), (3, 4, 4), (2, 4, 3),
-                                                     (2, 8, 1), (1, 1, 0)])
-def test_partials_chunk_plan(batch, h_kv, budget_units):
-    """Every (batch row, kv head) unit lands in exactly one chunk, chunks
-    stay within the budget unless one unit alone exceeds it, and a budget
-    that holds everything gives a single chunk."""
-    from moba.chunking import plan_chunks
+@pytest.mark.parametrize("batch,h_kv,group,budget", [(1, 4, 1, 100), (2, 4, 1, 8), (3, 4, 1, 4),
+                                                    (2, 4, 1, 3), (2, 8, 1, 1), (1, 1, 1, 0),
+                                                    (2, 2, 4, 0.5), (1, 3, 8, 0.25), (1, 2, 8, 0.3),
+                                                    (2, 2, 4, 0)])
+def test_partials_chunk_plan(batch, h_kv, group, budget):
+    """Every (batch row, query head) lands in exactly one chunk, chunks stay
+    within the budget unless one query head of one row alone exceeds it, a
+    chunk splits a kv head's group only when it holds that kv head alone,
+    and a budget that holds everything gives a single chunk."""
+    from moba.chunking import plan_chunks, query_heads
 
-    unit = 1000
-    chunks = plan_chunks(batch, h_kv, unit, budget_units * unit)
-    seen = [(b, h) for b0, b1, h0, h1 in chunks for b in range(b0, b1) for h in range(h0, h1)]
-    assert sorted(seen) == [(b, h) for b in range(batch) for h in range(h_kv)]
-    for b0, b1, h0, h1 in chunks:
-        assert (b1 - b0) * (h1 - h0) * unit <= max(unit, budget_units * unit)
+    unit = 1000 * group  # bytes of one (row, kv head) unit: `group` query heads
+    chunks = plan_chunks(batch, h_kv, unit, int(budget * unit), group=group)
+    seen = [(b, h) for c in chunks for b in range(c[0], c[1])
+            for h in range(*query_heads(c, group))]
+    assert sorted(seen) == [(b, h) for b in range(batch) for h in range(h_kv * group)]
+    for b0, b1, h0, h1, j0, j1 in chunks:
+        heads = (h1 - h0) * group if (j0, j1) == (0, group) else j1 - j0
+        assert (b1 - b0) * heads * (unit // group) <= max(unit // group, budget * unit)
         assert b1 - b0 == 1 or (h0, h1) == (0, h_kv)   # rectangles: whole rows or one row
-    if budget_units >= batch * h_kv:
-        assert chunks == [(0, batch, 0, h_kv)]
+        assert (j0, j1) == (0, group) or h1 - h0 == 1  # a split group: one kv head
+    if budget >= batch * h_kv:
+        assert chunks == [(0, batch, 0, h_kv, 0, group)]

@@ -277,12 +277,14 @@ def test_sdpa_dense_packed_equals_each_sequence_alone(device):
 
 
 @pytest.mark.parametrize("shape,h_kv,units", [((2, 1024, 8, 64), 2, 1), ((3, 768, 4, 64), 4, 4),
-                                              ((1, 1024, 8, 128), 4, 2)])
+                                              ((1, 1024, 8, 128), 4, 2),
+                                              ((1, 1024, 8, 128), 2, 0.5),   # 2 of 4 heads
+                                              ((2, 768, 8, 64), 1, 0.2)])    # 1 of 8 heads
 def test_chunked_partials_equal_one_pass(device, monkeypatch, shape, h_kv, units):
     """Per-slot buffers bounded to `units` (batch row, kv head) units: the
-    forward is bitwise the unchunked one (every stage works per row and kv
-    head), the gradients agree within the bf16 bars (dK / dV sum a column's
-    entries in an order the atomic CSC build does not fix)."""
+    forward is bitwise the unchunked one (every stage works per row and
+    query head), the gradients agree within the bf16 bars (below one unit
+    the query heads of a kv head run in subsets whose dK / dV are added)."""
     from moba.chunking import ENV_BUDGET, unit_bytes
 
     q, k, v, do = make_qkv(shape, torch.bfloat16, seed=4, n=4)
@@ -300,13 +302,18 @@ def test_chunked_partials_equal_one_pass(device, monkeypatch, shape, h_kv, units
     monkeypatch.setenv(ENV_BUDGET, str(1 << 40))
     whole = run()
     unit = unit_bytes(shape[1], shape[2] // h_kv, shape[3], cfg.slots(), 2)
-    monkeypatch.setenv(ENV_BUDGET, str(units * unit))
+    monkeypatch.setenv(ENV_BUDGET, str(int(units * unit)))
     chunked = run()
     assert torch.equal(whole[0], chunked[0]) and torch.equal(whole[1], chunked[1])
     assert torch.equal(whole[0], whole[1])
     for a, b in zip(whole[2:], chunked[2:]):
-        assert max_abs_error(a.float(), b.float()) <= BF16_MAX_ABS
-        assert mean_abs_error(a.float(), b.float()) <= BF16_MEAN_ABS
+        # Below one unit each head subset's dK / dV is rounded to bf16 before
+        # the subsets are added: bars scaled to the gradient's magnitude.
+        scale = (max(1.0, float(a.float().abs().max())), max(1.0, float(a.float().abs().mean())))
+        if units >= 1:
+            scale = (1.0, 1.0)
+        assert max_abs_error(a.float(), b.float()) <= BF16_MAX_ABS * scale[0]
+        assert mean_abs_error(a.float(), b.float()) <= BF16_MEAN_ABS * scale[1]
 
 
 def test_chunked_partials_packed(device, monkeypatch):
