@@ -90,6 +90,31 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * moba_gate without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Same arguments, semantics and output as moba_gate; its scratch (queue
+ * counter, kbar norms, one 8-byte queue entry per query) is a static device
+ * array of about 16 MiB that each GPU the library runs on holds until the
+ * process ends. Limits: batch * h_q * rows_per_seq <=
+ * MOBA_GATE_STATIC_MAX_QUERIES and batch * h_q <= MOBA_GATE_STATIC_MAX_NORMS
+ * (rows_per_seq = seq_len, or max_seqlen when packed); larger calls return
+ * MOBA_ERR_WORKSPACE. The call allocates nothing. Every call on one GPU
+ * shares that GPU's array (the call clears what must start at zero), so
+ * calls that overlap in time on one GPU (different streams, or host
+ * threads) race; serialise them. `stream` must belong to the current
+ * device.
+ */
+#define MOBA_GATE_STATIC_MAX_QUERIES 2097152
+#define MOBA_GATE_STATIC_MAX_NORMS 4096
+int moba_gate_noalloc(const void* q, const void* kbar, int32_t* block_idx,
+                      const int32_t* cu_seqlens, int64_t batch, int64_t seq_len,
+                      int64_t max_seqlen, int64_t h_q, int64_t h_kv,
+                      int64_t head_dim, int64_t n_blocks, int64_t block_size,
+                      int64_t slots, int64_t take, int always_current, int dtype,
+                      void* stream);
+
+/*
  * CSC transpose of block_idx into per-(row, kv head, block) columns:
  * col_nnz [R, Hkv, nb], col_offsets [R, Hkv, nb + 1] (exclusive prefix
  * sum), row_indices / head_indices / slot_of_pair [R, Hkv, cap] with

@@ -45,6 +45,8 @@
 //   registers.
 #include "common.h"
 
+#include <mutex>
+
 namespace moba {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -906,6 +908,80 @@ extern "C" size_t moba_gate_workspace_size(int64_t batch, int64_t seq_len, int64
   // counter + norms (bounded by batch * h_q floats) + one queue entry per query.
   size_t norms = (sizeof(float) * batch * h_q + 255) & ~size_t(255);
   return 256 + norms + sizeof(int64_t) * static_cast<size_t>(batch * h_q * seq_len);
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the gate's scratch (queue counter, kbar norms,
+// queue) lives in a file-scope device array instead of a caller workspace.
+// Each device holds its own copy at its own address; host code takes that
+// address once per device with hipGetSymbolAddress and never uses the
+// array's name (on the host the name is a stand-in, not a device address).
+// ---------------------------------------------------------------------------
+namespace moba {
+
+constexpr size_t kStaticNormBytes = sizeof(float) * MOBA_GATE_STATIC_MAX_NORMS;
+constexpr size_t kStaticBytes =
+    256 + kStaticNormBytes + sizeof(int64_t) * size_t(MOBA_GATE_STATIC_MAX_QUERIES);
+
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Address of the current device's copy of `scratch`, taken on the first
+// call on that device.
+static int static_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(MOBA_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MOBA_ERR_UNSUPPORTED, "device ordinal beyond the static scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MOBA_ERR_LAUNCH,
+                  std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOBA_OK;
+}
+
+}  // namespace moba
+
+extern "C" int moba_gate_noalloc(const void* q, const void* kbar, int32_t* block_idx,
+                                 const int32_t* cu_seqlens, int64_t batch,
+                                 int64_t seq_len, int64_t max_seqlen, int64_t h_q,
+                                 int64_t h_kv, int64_t head_dim, int64_t n_blocks,
+                                 int64_t block_size, int64_t slots, int64_t take,
+                                 int always_current, int dtype, void* stream) {
+  using namespace moba;
+  Geometry g;
+  int st = make_geometry(&g, batch, seq_len, max_seqlen, h_q, h_kv, head_dim, n_blocks,
+                         block_size, slots, cu_seqlens);
+  if (st) return st;
+  const int64_t queries = g.rows * g.h_q * g.rows_per_seq;
+  if (queries > MOBA_GATE_STATIC_MAX_QUERIES)
+    return fail(MOBA_ERR_WORKSPACE,
+                "moba_gate_noalloc: " + std::to_string(queries) +
+                    " query rows (batch * h_q * rows per sequence) exceed the static "
+                    "scratch limit of " + std::to_string(MOBA_GATE_STATIC_MAX_QUERIES));
+  if (g.rows * g.h_q > MOBA_GATE_STATIC_MAX_NORMS ||
+      moba_gate_workspace_size(g.rows, g.rows_per_seq, g.h_q) > kStaticBytes)
+    return fail(MOBA_ERR_WORKSPACE,
+                "moba_gate_noalloc: " + std::to_string(g.rows * g.h_q) +
+                    " (row, query head) pairs exceed the static scratch limit of " +
+                    std::to_string(MOBA_GATE_STATIC_MAX_NORMS));
+  void* ws = nullptr;
+  st = static_scratch(&ws);
+  if (st) return st;
+  return moba_gate(q, kbar, block_idx, cu_seqlens, batch, seq_len, max_seqlen, h_q, h_kv,
+                   head_dim, n_blocks, block_size, slots, take, always_current, dtype, ws,
+                   kStaticBytes, stream);
 }
 
 extern "C" int moba_gate(const void* q, const void* kbar, int32_t* block_idx,

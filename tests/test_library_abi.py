@@ -64,3 +64,13 @@ def test_workspace_queries_are_host_only():
     chunk = -(-2 * tiles // 64)
     assert lib.moba_csc_workspace_size(2, 1 << 22, 4, 2, 32768, 8) == \
         4 * 2 * 16384 * (4 * tiles + 2 * (-(-2 * tiles // chunk)))
+
+
+def test_noalloc_gate_rejects_sizes_past_its_static_scratch():
+    lib = _lib.load()
+    # [1, 524288 + 256, 4, 64]: 2^21 + 1024 query rows, past the 2^21 limit;
+    # rejected on the host before any device call.
+    rc = lib.moba_gate_noalloc(None, None, None, None, 1, 524288 + 256, 524288 + 256, 4, 4,
+                               64, 4099, 128, 8, 7, 1, 0, None)
+    assert rc == _lib.MOBA_ERR_WORKSPACE
+    assert b"static scratch limit" in lib.moba_last_error()
