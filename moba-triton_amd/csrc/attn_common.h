@@ -78,6 +78,10 @@ __device__ inline Column resolve_column(const AttnArgs& a, int64_t x, int64_t rh
   const int64_t e0 = n_all * s / c.nseg, e1 = n_all * (s + 1) / c.nseg;
   c.n = c.skip ? 0 : static_cast<int32_t>(e1 - e0);
   c.lo = rh * a.cap + a.col_offsets[rh * (a.n_blocks + 1) + c.blk] + e0;
+  // A column past its sequence's last block (packed sequences shorter than
+  // max_seqlen; n_blocks above cdiv(S, bs)) holds no keys: key_end = key0,
+  // and key0 / tok0 may then lie past the tensor, so no kernel may address
+  // K or V of such a column.
   if (a.cu) {
     const int64_t bos = a.cu[c.r], eos = a.cu[c.r + 1];
     c.key0 = bos + c.blk * a.bs;                     // packed: global tokens
@@ -88,6 +92,7 @@ __device__ inline Column resolve_column(const AttnArgs& a, int64_t x, int64_t rh
     c.key_end = c.key0 + a.bs < a.S ? c.key0 + a.bs : a.S;
     c.tok0 = c.r * a.S + c.key0;
   }
+  if (c.key_end < c.key0) c.key_end = c.key0;
   return c;
 }
 

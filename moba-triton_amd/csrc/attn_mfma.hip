@@ -434,6 +434,9 @@ bwd_mfma_kernel(AttnArgs a) {
   const uint16_t* Qg = static_cast<const uint16_t*>(a.q);
   const uint16_t* Og = static_cast<const uint16_t*>(a.dout);
   const int key_lim = static_cast<int>(c.key_end - c.key0);
+  // No keys (a column past its sequence): no query selects it and there is
+  // no dK / dV to write; its K / V rows would lie past the tensor.
+  if (key_lim <= 0) return;  // uniform
 
   const int lane = tid & 63;
   const int wave = tid >> 6;

@@ -153,11 +153,15 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
     Kt[i] = ok ? Elem<T>::load(K, off) : 0.f;
     Vt[i] = ok ? Elem<T>::load(V, off) : 0.f;
   }
-  // Accumulators for the (key, feature) elements this thread owns.
+  // Accumulators for the (key, feature) elements this thread owns. dK / dV
+  // sum over every query of the column (thousands at long sequences): the
+  // float32 path accumulates in float64 so the sum's rounding stays far
+  // below its 1e-5 bar; the 16-bit paths round to 8 or 11 bits anyway.
+  using Acc = typename std::conditional<sizeof(T) == 4, double, float>::type;
   constexpr int kMaxOwn = (kKT * 128) / 256;
-  float dk[kMaxOwn], dv[kMaxOwn];
+  Acc dk[kMaxOwn], dv[kMaxOwn];
 #pragma unroll
-  for (int u = 0; u < kMaxOwn; ++u) { dk[u] = 0.f; dv[u] = 0.f; }
+  for (int u = 0; u < kMaxOwn; ++u) { dk[u] = 0; dv[u] = 0; }
   const int own = static_cast<int>((kKT * D) / 256);
   for (int32_t e0 = 0; e0 < c.n; e0 += kBE) {
     __syncthreads();
@@ -200,10 +204,10 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
     for (int u = 0; u < own; ++u) {
       const int64_t i = threadIdx.x + static_cast<int64_t>(u) * blockDim.x;
       const int64_t j = i / D, d = i % D;
-      float adk = dk[u], adv = dv[u];
+      Acc adk = dk[u], adv = dv[u];
       for (int e = 0; e < kBE; ++e) {
-        adv = fmaf(Ps[e * kKT + j], Os[e * D + d], adv);
-        adk = fmaf(Gs[e * kKT + j], Qs[e * D + d], adk);
+        adv += static_cast<Acc>(Ps[e * kKT + j]) * static_cast<Acc>(Os[e * D + d]);
+        adk += static_cast<Acc>(Gs[e * kKT + j]) * static_cast<Acc>(Qs[e * D + d]);
       }
       dk[u] = adk;
       dv[u] = adv;
@@ -216,8 +220,8 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
     const int64_t j = i / D, d = i % D;
     if (kt0 + j >= a.bs || c.key0 + kt0 + j >= c.key_end) continue;
     const int64_t off = ((c.tok0 + kt0 + j) * a.h_kv + c.hk) * D + d;
-    Elem<T>::store(dK, off, dk[u] * a.scale);
-    Elem<T>::store(dV, off, dv[u]);
+    Elem<T>::store(dK, off, static_cast<float>(dk[u] * static_cast<Acc>(a.scale)));
+    Elem<T>::store(dV, off, static_cast<float>(dv[u]));
   }
 }
 

@@ -33,14 +33,19 @@ class OursBackend:
             if not torch.cuda.is_available():
                 return False, "no GPU device"
             arch = device_arch(0)
+            # The wording of both rejections below is what the reference's
+            # registry tests match (tests/test_registry.py:148-164): "tensor-core"
+            # for a dtype without a kernel, "tl.dot" for a block below the tile.
+            if cfg.dtype not in KERNEL_DTYPES:
+                return False, (f"dtype {cfg.dtype} has no tensor-core (MFMA) path; these "
+                               "kernels compute in bfloat16, float16 or float32")
             ok, reason = supports_dtype(cfg.dtype, arch.split(":")[0] or TARGET_ARCH)
             if not ok:
                 return False, reason
-            if cfg.dtype not in KERNEL_DTYPES:
-                return False, f"dtype {cfg.dtype} has no kernel path"
             if cfg.block_size < TENSOR_CORE_TILE:
-                return False, (f"block_size {cfg.block_size} is below the MFMA tile "
-                               f"minimum of {TENSOR_CORE_TILE}")
+                return False, (f"block_size {cfg.block_size} is below the MFMA tile minimum "
+                               f"(the tl.dot minimum of the Triton reference) of "
+                               f"{TENSOR_CORE_TILE}")
             ok, reason = _lib.available()
             if not ok:
                 return False, reason

@@ -5,7 +5,9 @@ key, the anchor of the attainment figure (speedup over dense divided by the
 speedup the sparsity pattern makes available, reference `bench/suite.py:1-12,
 549-583`). Only the fused SDPA kernels are allowed: the math path would
 materialise an S x S score matrix, which at the benchmark lengths does not
-fit; with no fused kernel for a shape the call raises instead.
+fit; it is allowed only up to MATH_MAX_SEQ tokens (small test shapes in
+dtypes without a fused kernel), and past that a shape with no fused kernel
+raises.
 """
 
 import torch
@@ -17,6 +19,7 @@ from moba.config import MoBAConfig
 from moba.gqa import head_group_size
 
 FUSED = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+MATH_MAX_SEQ = 8192
 
 
 class SdpaDenseBackend:
@@ -42,7 +45,10 @@ class SdpaDenseBackend:
         if group > 1:
             k, v = (t.repeat_interleave(group, dim=2) for t in (k, v))
         qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))
-        with sdpa_kernel(FUSED):
+        # The math path materialises S x S scores: allowed only where that is
+        # small (dtypes without a fused kernel, e.g. float64, at test sizes).
+        allowed = FUSED + ([SDPBackend.MATH] if q.shape[1] <= MATH_MAX_SEQ else [])
+        with sdpa_kernel(allowed):
             out = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
         return out.transpose(1, 2)
 

@@ -6,14 +6,14 @@ moba_topk)` takes packed `[T, H, D]` tensors and returns `[T, H, D]`. Its
 `moba_topk` counts the query's own block (MoonshotAI's convention, which is
 `MoBAConfig`'s default `top_k_includes_current=True`). Differentiable.
 
-The backend registered here wraps a padded batch into that signature, the way
-the reference adapter does, so harnesses see one more MoBA implementation.
+Only the signature lives here. The reference registers "triton_moba" as a
+vendored third-party backend (`implementations/triton_moba.py:32-36`); this
+build registers nothing under that name, so a harness comparing backends never
+reports these kernels as a second implementation.
 """
 
 import torch
 
-from implementations.base import register
-from implementations.ours import OursBackend
 from moba.config import MoBAConfig
 from moba.kernels.attention import moba_attention
 
@@ -33,26 +33,3 @@ def moba_attn_varlen_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 # Name kept by the reference adapter's caller.
 moba_attn_varlen = moba_attn_varlen_triton
-
-
-class TritonMoBABackend(OursBackend):
-    """Padded [B, S, H, D] batches through the varlen signature."""
-
-    name = "triton_moba"
-    vendored = False
-    computes_moba = True
-
-    def forward(self, q, k, v, cfg: MoBAConfig) -> torch.Tensor:
-        self._require(cfg)
-        b, s, h, d = q.shape
-        cu = torch.arange(0, (b + 1) * s, s, device=q.device, dtype=torch.int32)
-        out = moba_attn_varlen_triton(q.reshape(b * s, h, d), k.reshape(b * s, -1, d),
-                                      v.reshape(b * s, -1, d), cu, s, cfg.block_size,
-                                      cfg.top_k)
-        return out.view(b, s, h, d)
-
-    def forward_grad(self, q, k, v, cfg: MoBAConfig) -> torch.Tensor:
-        return self.forward(q, k, v, cfg)
-
-
-register(TritonMoBABackend())

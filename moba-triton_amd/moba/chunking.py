@@ -36,11 +36,17 @@ def partials_budget(device) -> int:
     return min(total // 4, free // 2)
 
 
-def unit_bytes(rows_per_seq: int, group: int, head_dim: int, slots: int, elem: int) -> int:
-    """Per-slot buffer bytes of one (batch row, kv head) unit: the value rows
+def unit_bytes(tokens: int, group: int, head_dim: int, slots: int, elem: int) -> int:
+    """Per-slot buffer bytes of one (batch row, kv head) unit of `tokens`
+    tokens (the row's whole token axis; T for packed input): the value rows
     (forward partials, then dQ partials: the larger of the two phases) plus
-    the 8-byte (m, l) records."""
-    return rows_per_seq * group * slots * (head_dim * elem + 8)
+    the 8-byte (m, l) records.
+
+    Not counted: the CSC index each chunk keeps until backward (12 bytes per
+    (query, slot) entry slot, sized sequences x max_seqlen x slots per kv
+    head's group when packed). It lives for the whole step whatever the
+    chunking, so splitting cannot reduce it."""
+    return tokens * group * slots * (head_dim * elem + 8)
 
 
 def plan_chunks(batch: int, h_kv: int, unit: int, budget: int,
@@ -69,3 +75,13 @@ def query_heads(chunk, group: int) -> tuple[int, int]:
     """First and past-the-last query head of a chunk."""
     _, _, hk0, hk1, j0, j1 = chunk
     return hk0 * group + j0, (hk1 - 1) * group + j1
+
+
+def plan_call(q_shape: tuple, h_kv: int, slots: int, elem: int,
+              budget: int) -> list[tuple[int, int, int, int, int, int]]:
+    """Chunks of a call on q of shape [B, S, Hq, D] (packed: [1, T, Hq, D]):
+    units of one batch row's S tokens per kv head, value rows of `elem`
+    bytes."""
+    b, s, h_q, d = q_shape
+    group = h_q // h_kv
+    return plan_chunks(b, h_kv, unit_bytes(s, group, d, slots, elem), budget, group=group)

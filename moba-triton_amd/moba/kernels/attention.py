@@ -9,7 +9,7 @@ receives no gradient (`attention.py:33-38`): routing is a hard top-k.
 import torch
 
 from moba import _lib
-from moba.chunking import partials_budget, plan_chunks, query_heads, unit_bytes
+from moba.chunking import partials_budget, plan_call, query_heads
 from moba.config import MoBAConfig
 from moba.kernels.moba_bwd import moba_backward
 from moba.kernels.moba_fwd import _validate, attend_partials, combine_partials
@@ -21,17 +21,23 @@ def _piece(t, b0, b1, h0, h1):
     return t[b0:b1, :, h0:h1].contiguous()
 
 
-def forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen):
+def forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen, partials_dtype=None):
     """The chunks (b0, b1, hk0, hk1, j0, j1) -- batch rows, kv heads, and
     query heads within each kv head's group -- the per-slot buffers of this
     call are split into (one chunk when they fit the budget of
-    `moba.chunking`)."""
+    `moba.chunking`).
+
+    The per-slot buffers are [B, Hq, S, slots(, D)] over the tensor's token
+    axis, so a unit (one batch row, one kv head) spans all S tokens of the
+    row; packed input is one row of T = S tokens, whatever max_seqlen is.
+    Value rows are sized in the larger of q's dtype (the dQ partials) and
+    `partials_dtype` (the forward's part_acc)."""
     _lib.require_gpu(q, k, v)  # raises before any device query on host tensors
-    b, s, h_q, d = q.shape
     h_kv = k.shape[2]
-    rps = max_seqlen if cu_seqlens is not None else s
-    unit = unit_bytes(rps, h_q // h_kv, d, cfg.slots(), q.element_size())
-    return plan_chunks(b, h_kv, unit, partials_budget(q.device), group=h_q // h_kv)
+    elem = q.element_size()
+    if partials_dtype is not None:
+        elem = max(elem, torch.empty((), dtype=partials_dtype).element_size())
+    return plan_call(tuple(q.shape), h_kv, cfg.slots(), elem, partials_budget(q.device))
 
 
 class MoBAAttentionFunction(torch.autograd.Function):

@@ -175,7 +175,8 @@ def moba_forward(q, k, v, cfg: MoBAConfig, index: CSCIndex | None = None,
     # (batch row, kv head[, query heads]) chunks (moba.chunking).
     from moba.chunking import query_heads
     from moba.kernels.attention import _piece, forward_chunks
-    chunks = forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen)
+    chunks = forward_chunks(q, k, v, cfg, causal, cu_seqlens, max_seqlen,
+                            partials_dtype=partials_dtype)
     group = q.shape[2] // k.shape[2]
     out = torch.empty_like(q) if len(chunks) > 1 else None
     for chunk in chunks:

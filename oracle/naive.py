@@ -19,7 +19,7 @@ __all__ = [
     "round_to_dtype", "pool_blocks", "gate_scores", "select_from_scores",
     "gate_select", "moba_selection", "mask_to_indices", "indices_to_mask",
     "moba_attention", "moba_attention_sparse", "build_csc", "csc_to_mask",
-    "combine_reference", "slots_per_query",
+    "combine_reference", "slots_per_query", "sparse_grads",
 ]
 
 
@@ -324,6 +324,95 @@ def moba_attention_sparse(q, k, v, block_idx, block_size, rows=None,
     probs = torch.exp(logits - lse[..., None])
     out = torch.einsum("bhrj,bhrjd->bhrd", probs, vv)
     return out.permute(0, 2, 1, 3), lse
+
+
+def sparse_grads(q, k, v, do, block_idx, block_size, rows, key_blocks=None,
+                 dtype=torch.float64, max_gather_bytes=1 << 30, key_users_only=False):
+    """Explicit gradients of (out * dO).sum() for the query rows `rows` of a
+    batch-1 sequence, without autograd: the same attention as
+    `moba_attention_sparse` differentiated by hand, in the backward's
+    formulation (reference `src/moba/kernels/moba_bwd.py:216-394`):
+    p = softmax(q.K * D^-1/2), O = p.V, delta = O.dO, dp = dO.V,
+    ds = p (dp - delta), dq = ds.K * D^-1/2, dK += ds^T q * D^-1/2,
+    dV += p^T dO.
+
+    Every product is formed in `dtype` (float64 for ground truth; bfloat16
+    gives the same-dtype oracle of the tolerance policy) and every sum over
+    queries (dK, dV) or keys (dq, O) is accumulated in float32 or float64 and
+    rounded once to `dtype`, as one matmul in that dtype would be.
+
+    Only rows whose queries appear in `rows` contribute; dK / dV are
+    accumulated for the keys of `key_blocks` (block ids; None = every key).
+    Returns (out [1, R, H, D], dq [1, R, H, D], dk [1, S, Hkv, D],
+    dv [1, S, Hkv, D]) in `dtype`; dk / dv hold zeros outside `key_blocks`.
+    With `key_users_only`, a (row, head) pair whose selection holds none of
+    `key_blocks` is skipped (it adds nothing to those keys) and its out / dq
+    stay zero.
+    """
+    b, s, h, d = q.shape
+    if b != 1:
+        raise ValueError("sparse_grads takes one sequence (batch 1)")
+    h_kv = k.shape[2]
+    g = head_group_size(h, h_kv)
+    acc_t = torch.float64 if dtype == torch.float64 else torch.float32
+    scale = torch.tensor(d ** -0.5, dtype=dtype)
+    rows = torch.as_tensor(rows, dtype=torch.int64)
+    r_all = rows.numel()
+    slots = block_idx.shape[-1]
+    width = slots * block_size
+    dk = torch.zeros(s, h_kv, d, dtype=acc_t)
+    dv = torch.zeros(s, h_kv, d, dtype=acc_t)
+    out = torch.zeros(r_all, h, d, dtype=dtype)
+    dq = torch.zeros(r_all, h, d, dtype=dtype)
+    qx, kx, vx, dox = (t[0].to(dtype) for t in (q, k, v, do))
+    keys_wanted = None
+    if key_blocks is not None:
+        keys_wanted = torch.zeros(-(-s // block_size) + 1, dtype=torch.bool)
+        keys_wanted[torch.as_tensor(key_blocks, dtype=torch.int64)] = True
+    chunk = max(1, max_gather_bytes // (width * d * 8 * 2))
+    key_off = torch.arange(block_size)
+    for hq in range(h):
+        hk = hq // g
+        k_h, v_h = kx[:, hk].contiguous(), vx[:, hk].contiguous()
+        todo = torch.arange(r_all)
+        if key_users_only and keys_wanted is not None:
+            ids = block_idx[0, hq, rows].long()
+            todo = torch.nonzero(((ids >= 0) & keys_wanted[ids.clamp(min=0)]).any(-1)).flatten()
+        for lo in range(0, todo.numel(), chunk):
+            sel = todo[lo:lo + chunk]
+            r = rows[sel]
+            blk = block_idx[0, hq, r].long()                              # [R, slots]
+            kpos = blk.clamp(min=0)[..., None] * block_size + key_off     # [R, slots, bs]
+            ok = (blk >= 0)[..., None] & (kpos < s) & (kpos <= r.view(-1, 1, 1))
+            kpos = kpos.clamp(max=s - 1).reshape(-1, width)
+            ok = ok.reshape(-1, width)
+            flat = kpos.reshape(-1)
+            kg = k_h.index_select(0, flat).view(-1, width, d)             # [R, W, D]
+            vg = v_h.index_select(0, flat).view(-1, width, d)
+            qr, dor = qx[r, hq], dox[r, hq]                               # [R, D]
+            logits = torch.einsum("rd,rwd->rw", qr, kg) * scale
+            logits = logits.masked_fill(~ok, float("-inf"))
+            p = torch.softmax(logits.to(acc_t), dim=-1).to(dtype)
+            o = torch.einsum("rw,rwd->rd", p, vg)
+            delta = (o.to(acc_t) * dor.to(acc_t)).sum(-1, keepdim=True).to(dtype)
+            dp = torch.einsum("rd,rwd->rw", dor, vg)
+            ds = p * (dp - delta)
+            out[sel, hq] = o
+            dq[sel, hq] = (torch.einsum("rw,rwd->rd", ds.to(acc_t), kg.to(acc_t))
+                           * scale.to(acc_t)).to(dtype)
+            live = ok
+            if keys_wanted is not None:
+                live = live & keys_wanted[blk.clamp(min=0)].repeat_interleave(block_size, -1)
+            if not bool(live.any()):
+                continue
+            rr, ww = torch.nonzero(live, as_tuple=True)
+            kp = kpos[rr, ww]
+            dk_c = (ds[rr, ww, None] * qr[rr] * scale).to(dtype)
+            dv_c = (p[rr, ww, None] * dor[rr]).to(dtype)
+            dk[:, hk].index_add_(0, kp, dk_c.to(acc_t))
+            dv[:, hk].index_add_(0, kp, dv_c.to(acc_t))
+    return (out.unsqueeze(0), dq.unsqueeze(0), dk.to(dtype).unsqueeze(0),
+            dv.to(dtype).unsqueeze(0))
 
 
 # ---------------------------------------------------------------------------

@@ -42,14 +42,16 @@ def test_head_group_and_expand():
 
 def test_registry_contract():
     names = [b.name for b in implementations.all_backends()]
-    assert "ours" in names and "triton_moba" in names and "sdpa_dense" in names
+    assert {"ours", "naive_torch", "sdpa_dense"} <= set(names)
+    # The vendored third-party name is not claimed by this build's kernels.
+    assert "triton_moba" not in names
     assert get_backend("ours").computes_moba and not get_backend("sdpa_dense").computes_moba
     cfg = MoBAConfig(block_size=128, top_k=8)
     for b in implementations.all_backends():
         assert isinstance(b, Backend)
         ok, reason = b.is_available(cfg)  # never raises
         assert isinstance(ok, bool) and isinstance(reason, str)
-        if not torch.cuda.is_available():
+        if not torch.cuda.is_available() and b.name != "naive_torch":
             assert not ok and reason
     with pytest.raises(ValueError):
         register(get_backend("ours"))
@@ -151,3 +153,21 @@ def test_partials_chunk_plan(batch, h_kv, group, budget):
         assert (j0, j1) == (0, group) or h1 - h0 == 1  # a split group: one kv head
     if budget >= batch * h_kv:
         assert chunks == [(0, batch, 0, h_kv, 0, group)]
+
+
+def test_chunk_plan_sizes_packed_units_by_total_tokens():
+    """Packed input keeps [1, Hq, T, slots, D] partials: a unit is all T
+    tokens of the one row, not max_seqlen of them."""
+    from moba.chunking import plan_call, unit_bytes
+    t, max_seqlen, h, d, slots = 524288, 32768, 4, 64, 8
+    unit = unit_bytes(t, 1, d, slots, 2)
+    assert unit == t * slots * (d * 2 + 8)
+    # Budget fits one kv head's T-token unit but not two: one chunk per head.
+    chunks = plan_call((1, t, h, d), h, slots, 2, budget=unit + unit // 2)
+    assert chunks == [(0, 1, hk, hk + 1, 0, 1) for hk in range(h)]
+    # Sized by max_seqlen (16x too small) it would have taken one chunk.
+    assert 4 * unit_bytes(max_seqlen, 1, d, slots, 2) <= unit + unit // 2
+    # float32 part_acc doubles the value rows.
+    assert plan_call((1, t, h, d), h, slots, 4, budget=unit + unit // 2) == \
+        [(0, 1, hk, hk + 1, 0, 1) for hk in range(h)]
+    assert len(plan_call((1, t, h, d), h, slots, 4, budget=2 * unit)) == 4

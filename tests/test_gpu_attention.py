@@ -193,6 +193,47 @@ def test_backward_fp32_matches_autograd(device):
         assert max_abs_error(ours, tr) <= FP32_MAX_ABS
 
 
+@pytest.mark.parametrize("shape,h_kv,bs,tk", [((1, 1024, 8, 64), 2, 128, 4),
+                                              ((1, 2048, 4, 64), 4, 128, 8),
+                                              ((1, 1024, 4, 128), 1, 64, 3)])
+def test_backward_fp32_gqa_and_bs128_match_autograd(device, shape, h_kv, bs, tk):
+    """The float32 path at 1e-5: GQA groups of 4 and 8 query heads per kv
+    head, D 128, and the headline's block size 128 / top-k 8."""
+    cfg = MoBAConfig(block_size=bs, top_k=tk, dtype=torch.float32)
+    q, k, v = make_qkv(shape, torch.float32, seed=23, device=device)
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    g = make_qkv(shape, torch.float32, seed=24, device=device, n=1)[0]
+    sel = oracle_selection(q, k, cfg)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = moba_attention(qq, kk, vv, cfg)
+    out.backward(g)
+    qc, kc, vc, gc = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v, g))
+    ref = O.moba_attention(qc, kc, vc, oracle_cfg(cfg), selected=sel, query_chunk=256)
+    ref.backward(gc.detach())
+    for name, ours, tr in (("out", out, ref), ("dq", qq.grad, qc.grad), ("dk", kk.grad, kc.grad),
+                           ("dv", vv.grad, vc.grad)):
+        assert max_abs_error(ours, tr) <= FP32_MAX_ABS, name
+
+
+def test_backward_fp32_packed_matches_autograd(device):
+    cfg = MoBAConfig(block_size=64, top_k=4, dtype=torch.float32)
+    lens = [500, 128, 700]
+    cu = torch.tensor([0, 500, 628, 1328], dtype=torch.int32, device=device)
+    q = make_qkv((1, 1328, 4, 64), torch.float32, seed=25, device=device, n=1)[0]
+    k, v = make_qkv((1, 1328, 2, 64), torch.float32, seed=26, device=device, n=2)
+    g = make_qkv((1, 1328, 4, 64), torch.float32, seed=27, device=device, n=1)[0]
+    sel = oracle_selection(q, k, cfg, cu_seqlens=cu)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = moba_attention(qq, kk, vv, cfg, cu_seqlens=cu, max_seqlen=max(lens))
+    out.backward(g)
+    qc, kc, vc, gc = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v, g))
+    ref = O.moba_attention(qc, kc, vc, oracle_cfg(cfg), selected=sel, cu_seqlens=cu.cpu())
+    ref.backward(gc.detach())
+    for name, ours, tr in (("out", out, ref), ("dq", qq.grad, qc.grad), ("dk", kk.grad, kc.grad),
+                           ("dv", vv.grad, vc.grad)):
+        assert max_abs_error(ours, tr) <= FP32_MAX_ABS, name
+
+
 def test_unselected_blocks_get_exactly_zero_gradient(device):
     cfg = MoBAConfig(block_size=64, top_k=2, always_select_current=False)
     shape = (1, 1024, 2, 64)

@@ -235,3 +235,52 @@ def test_sparsity_ratio_counts_the_selected_keys(s, bs, tk):
     want = attended / (i + 1).sum(dtype=torch.float64)
     got = sparsity_ratio(s, MoBAConfig(block_size=bs, top_k=tk))
     assert abs(got - want.item()) < 1e-12
+
+
+@pytest.mark.parametrize("h,hkv", [(2, 2), (4, 2)])
+def test_hand_gradients_equal_autograd_of_the_dense_form(h, hkv):
+    """`sparse_grads` (the explicit backward used at full sizes) against torch
+    autograd of the dense oracle: all rows and keys, then a row subset with
+    dK / dV restricted to some blocks."""
+    q, k, v = qkv(1, 333, h, 16, seed=6)
+    k, v = k[:, :, :hkv].contiguous(), v[:, :, :hkv].contiguous()
+    do = qkv(1, 333, h, 16, seed=7)[0]
+    c = cfg(32, 4)
+    sel = O.moba_selection(q, k, c)
+    idx = O.mask_to_indices(sel, 4)
+    lq, lk, lv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    ref = O.moba_attention(lq, lk, lv, c, selected=sel)
+    ref.backward(do)
+    out, dq, dk, dv = O.sparse_grads(q, k, v, do, idx, 32, torch.arange(333))
+    for got, want in ((out, ref.detach()), (dq, lq.grad), (dk, lk.grad), (dv, lv.grad)):
+        torch.testing.assert_close(got, want, rtol=0, atol=1e-12)
+    # A row subset: out and dq of those rows; dk / dv of blocks {0, 5} from
+    # every row that selected them equal autograd's on those keys.
+    rows = torch.tensor([0, 40, 200, 332])
+    out, dq, _, _ = O.sparse_grads(q, k, v, do, idx, 32, rows, max_gather_bytes=1 << 14)
+    torch.testing.assert_close(out, ref.detach()[:, rows], rtol=0, atol=1e-12)
+    torch.testing.assert_close(dq, lq.grad[:, rows], rtol=0, atol=1e-12)
+    users = torch.nonzero((idx[..., None] == torch.tensor([0, 5])).any(-1).any(-1).any(1)[0])
+    keys = torch.cat([torch.arange(0, 32), torch.arange(160, 192)])
+    for only in (False, True):
+        _, _, dk, dv = O.sparse_grads(q, k, v, do, idx, 32, users.flatten(), key_blocks=[0, 5],
+                                      key_users_only=only)
+        torch.testing.assert_close(dk[:, keys], lk.grad[:, keys], rtol=0, atol=1e-12)
+        torch.testing.assert_close(dv[:, keys], lv.grad[:, keys], rtol=0, atol=1e-12)
+        assert not bool(dk[:, 32:160].any()), "keys outside key_blocks must stay zero"
+
+
+def test_hand_gradients_in_bfloat16_track_float64():
+    """The same-dtype oracle: bfloat16 products, one rounding per sum. Its
+    error against float64 is of bfloat16 size, neither zero nor large."""
+    q, k, v = qkv(1, 256, 2, 64, seed=8)
+    do = qkv(1, 256, 2, 64, seed=9)[0]
+    q, k, v, do = (t.bfloat16().double() for t in (q, k, v, do))
+    idx = O.mask_to_indices(O.moba_selection(q, k, cfg(32, 4)), 4)
+    rows = torch.arange(256)
+    hi = O.sparse_grads(q, k, v, do, idx, 32, rows)
+    lo = O.sparse_grads(q, k, v, do, idx, 32, rows, dtype=torch.bfloat16)
+    for a, b in zip(lo, hi):
+        assert a.dtype is torch.bfloat16
+        err = (a.double() - b).abs().max().item()
+        assert 1e-5 < err < 5e-2 * max(1.0, b.abs().max().item()), err
