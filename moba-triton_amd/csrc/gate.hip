@@ -748,6 +748,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         jr[r] = u0 + r < nu ? static_cast<int>(su[(u0 + r) * 64]) : 0;
+        jr[r] = jr[r] < hz ? jr[r] : 0;  // ids come from this lane's buffers; a guard
         const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
 #pragma unroll
         for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
