@@ -12,6 +12,7 @@ S = 64K..512K beside the reference's published H100 numbers.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--seq S]
        [--no-sweep] [--no-cpu]
+       python bench.py --summarize-counters OUT.json DB... [--command CMD]
 """
 
 import argparse
@@ -38,6 +39,13 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs,
 # scaled by the same counters' reading for a plain copy of known size.
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_fwd_bwd_S524288.json"
+# SQ / GRBM counters per kernel from rocprofv3 --pmc runs of this script
+# (`--summarize-counters` writes it); the bench line reports the MFMA, VALU
+# and LDS utilisation they give beside the algorithmic figures.
+COUNTERS_FILE = ROOT / "profiles" / "counters_fwd_bwd_S524288.json"
+# MI355X: 8 XCDs x 32 CUs x 4 SIMDs. GRBM_GUI_ACTIVE arrives summed over the
+# XCDs, so GUI / 8 is the dispatch's clock count.
+XCDS, CUS, SIMDS_PER_CU = 8, 256, 4
 # Stage -> the kernel that dominates it (name as rocprofv3 reports it).
 STAGE_KERNEL = {
     "pool": "pool_kernel", "gate": "gate_mfma_kernel", "csc": "det_scatter_kernel",
@@ -70,6 +78,75 @@ def gate_flops(s, hq=HEADS, d=HEAD_DIM, bs=BLOCK):
         hz = min(t0 + 127, s - 1) // bs
         pairs += 128 * ((hz + 31) // 32) * 32
     return 2 * d * pairs * hq
+
+
+def _short_kernel(name):
+    """`void moba::gate_mfma_kernel<...>(...)` -> `gate_mfma_kernel`."""
+    return name.split("<")[0].split("(")[0].replace("void ", "").split("::")[-1]
+
+
+def summarize_counters(out_path, dbs, command):
+    """Reduces rocprofv3 `--pmc` databases (rocpd SQLite, one per counter
+    pass) to per-kernel averages per dispatch plus derived utilisation:
+
+    - mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x clocks)
+    - valu_busy = SQ_ACTIVE_INST_VALU / (256 CUs x clocks)
+    - lds_busy = SQ_LDS_IDX_ACTIVE / (256 CUs x clocks), of which
+      lds_bank_conflict_frac = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE
+    - waves_per_simd = 4 x SQ_WAVE_CYCLES (quad-cycles) / (1024 x clocks)
+    - per-wave instruction counts (SQ_INSTS_* / SQ_WAVES)
+    with clocks = GRBM_GUI_ACTIVE / 8 (the counter is summed over the XCDs).
+    These are rocprofv3's own MfmaUtil / VALUBusy / LdsUtil definitions.
+    """
+    import collections
+    import sqlite3
+
+    sums = collections.defaultdict(lambda: collections.defaultdict(list))
+    durs = collections.defaultdict(list)
+    for db in dbs:
+        con = sqlite3.connect(db)
+        q = "select kernel_name, counter_name, value, duration, dispatch_id from counters_collection"
+        seen = set()
+        for kname, cname, val, dur, did in con.execute(q):
+            k = _short_kernel(kname)
+            sums[k][cname].append(float(val))
+            if (db, did) not in seen:
+                seen.add((db, did))
+                durs[k].append(float(dur))
+        con.close()
+    kernels = {}
+    for k, cs in sums.items():
+        avg = {c: sum(v) / len(v) for c, v in cs.items()}
+        row = {"dispatches": len(durs[k]), "avg_duration_us": round(sum(durs[k]) / len(durs[k]) / 1e3, 2),
+               "counters": {c: round(v, 1) for c, v in sorted(avg.items())}}
+        clk = avg.get("GRBM_GUI_ACTIVE", 0.0) / XCDS
+        d = {}
+        if clk > 0:
+            simd_clk, cu_clk = clk * CUS * SIMDS_PER_CU, clk * CUS
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+                d["mfma_busy"] = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / simd_clk
+            if "SQ_ACTIVE_INST_VALU" in avg:
+                d["valu_busy"] = avg["SQ_ACTIVE_INST_VALU"] / cu_clk
+            if "SQ_LDS_IDX_ACTIVE" in avg:
+                d["lds_busy"] = avg["SQ_LDS_IDX_ACTIVE"] / cu_clk
+                if avg["SQ_LDS_IDX_ACTIVE"] > 0:
+                    d["lds_bank_conflict_frac"] = avg.get("SQ_LDS_BANK_CONFLICT", 0.0) / avg["SQ_LDS_IDX_ACTIVE"]
+            if "SQ_WAVE_CYCLES" in avg:  # quad-cycles summed over SIMDs
+                d["waves_per_simd"] = 4 * avg["SQ_WAVE_CYCLES"] / simd_clk
+            d["clock_ghz"] = clk / (row["avg_duration_us"] * 1e3)
+        waves = avg.get("SQ_WAVES")
+        if waves:
+            for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA",
+                      "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR"):
+                if c in avg:
+                    d[c.replace("SQ_INSTS_", "insts_per_wave_").lower()] = avg[c] / waves
+        row["derived"] = {n: round(v, 4) for n, v in d.items()}
+        kernels[k] = row
+    doc = {"command": command, "workload": "fwd+bwd [1,524288,4,64] bf16 bs128 k8",
+           "note": "averages per dispatch; one rocprofv3 --pmc pass per database",
+           "kernels": kernels}
+    Path(out_path).write_text(json.dumps(doc, indent=1) + "\n")
+    print(f"wrote {out_path}: {sorted(kernels)}")
 
 
 def make_inputs(s, dev, seed=0):
@@ -244,7 +321,14 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
+    ap.add_argument("--summarize-counters", nargs="+", metavar=("OUT_JSON", "DB"),
+                    help="reduce rocprofv3 --pmc databases to OUT_JSON and exit (no GPU)")
+    ap.add_argument("--command", default="", help="with --summarize-counters: the "
+                    "profiling command, recorded in OUT_JSON")
     args = ap.parse_args()
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters[0], args.summarize_counters[1:], args.command)
+        return
     if args.copy_probe:
         x = torch.empty(1 << 29, dtype=torch.int16, device="cuda:0").fill_(1)
         y = torch.empty_like(x)
@@ -296,6 +380,13 @@ def main():
             row["mfma_TFLOPs"] = round(gf / (t * 1e-3) / 1e12, 1)
             row["mfma_frac"] = round(gf / (t * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
         stage_rows[n] = row
+    if COUNTERS_FILE.exists():
+        ck = json.loads(COUNTERS_FILE.read_text()).get("kernels", {})
+        for n, row in stage_rows.items():
+            dv = ck.get(STAGE_KERNEL[n], {}).get("derived", {})
+            for key in ("mfma_busy", "valu_busy", "lds_busy"):
+                if key in dv:
+                    row["rocprof_" + key] = dv[key]
     print(f"[bench] stages {stage_rows}", file=sys.stderr, flush=True)
     dom = max(stages, key=stages.get)
     traffic = None
