@@ -211,6 +211,46 @@ def stage_times(s, dev, reps=5):
     return st
 
 
+def hierarchical_gate(s, dev, configs=((16, 8), (4, 8)), reps=5):
+    """The opt-in hierarchical gate (`MoBAConfig.gate_group` / `gate_open`)
+    beside the exact gate at S: device time of `gate_select` and recall --
+    the share of the exact gate's strictly-past selections it keeps -- on the
+    bench's i.i.d. keys (the worst case for any hierarchy) and on keys with
+    positional locality (a random walk along the sequence plus unit noise),
+    the two cases of the reference's `docs/gate-hierarchical-measurements.md`."""
+    from moba.config import MoBAConfig
+    from moba.kernels.gating import gate_select
+    from moba.kernels.pooling import pool_blocks
+
+    g = torch.Generator(device=dev).manual_seed(1)
+    shape = (1, s, HEADS, HEAD_DIM)
+    q = torch.randn(shape, generator=g, device=dev, dtype=torch.bfloat16)
+    k_iid = torch.randn(shape, generator=g, device=dev, dtype=torch.bfloat16)
+    walk = torch.randn(shape, generator=g, device=dev).mul_(0.05).cumsum_(1)
+    k_walk = (walk + torch.randn(shape, generator=g, device=dev)).to(torch.bfloat16)
+    del walk
+    exact_cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
+    own = (torch.arange(s, device=dev) // BLOCK).view(1, 1, s, 1)
+
+    def recall(sel, ref):
+        ref_ok = (ref >= 0) & (ref != own)
+        hit = (sel.unsqueeze(-1) == ref.unsqueeze(-2)).any(-2) & ref_ok
+        return float(hit.sum()) / max(1.0, float(ref_ok.sum()))
+
+    kbars = {"iid": pool_blocks(k_iid, exact_cfg), "walk": pool_blocks(k_walk, exact_cfg)}
+    exact = {n: gate_select(q, kb, exact_cfg) for n, kb in kbars.items()}
+    out = {"exact_gate_ms": round(timed(lambda: gate_select(q, kbars["iid"], exact_cfg),
+                                        reps, 1)[0], 4), "configs": []}
+    for group, opened in configs:
+        cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK, gate_group=group, gate_open=opened)
+        row = {"gate_group": group, "gate_open": opened,
+               "gate_ms": round(timed(lambda: gate_select(q, kbars["iid"], cfg), reps, 1)[0], 4)}
+        for n, kb in kbars.items():
+            row["recall_" + n] = round(recall(gate_select(q, kb, cfg), exact[n]), 4)
+        out["configs"].append(row)
+    return out
+
+
 def attainment(q, k, v, cfg, s, fwd_ms):
     """The reference's headline ratio (`bench/suite.py:1-12, 549-583`): the
     forward speedup over dense causal attention (torch SDPA, fused kernels
@@ -318,6 +358,8 @@ def main():
     ap.add_argument("--seq", type=int, default=524288)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-hier", action="store_true",
+                    help="skip the opt-in hierarchical gate's timing and recall")
     ap.add_argument("--cpu-rows", type=int, default=16384)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
@@ -408,6 +450,8 @@ def main():
                 "algorithmic": ab[dom]}
     total_alg = sum(ab.values())
     rows = [] if args.no_sweep else sweep(dev, SWEEP)
+    hier = None if args.no_hier else hierarchical_gate(s, dev)
+    torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline(s, args.cpu_rows)
     tokens = s  # query tokens per step (batch 1)
     line = {
@@ -427,6 +471,7 @@ def main():
                           "frac": round(total_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "stages": stage_rows,
         "sweep": rows,
+        "hierarchical_gate": hier,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

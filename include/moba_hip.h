@@ -90,6 +90,25 @@ int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Second stage of the opt-in hierarchical gate (never the default): for
+ * each query, the strictly-past blocks inside the super-blocks listed in
+ * super_idx [B, Hq, S, super_slots] (ascending super-block ids, -1 padded,
+ * as moba_gate emits them when run over super-block representatives with
+ * block size block_size * group), ranked by the gate's score and tie rule;
+ * the best `take` plus the own block (if always_current) go to block_idx
+ * [B, Hq, S, slots], ascending, -1 padded. super_slots * group <= 512;
+ * padded input only. The scheme is the coarse-to-fine selection the
+ * reference measured in docs/gate-hierarchical-measurements.md (no kernel
+ * there); the first stage is moba_pool over the block representatives and
+ * moba_gate over the result.
+ */
+int moba_gate_refine(const void* q, const void* kbar, const int32_t* super_idx,
+                     int32_t* block_idx, int64_t batch, int64_t seq_len, int64_t h_q,
+                     int64_t h_kv, int64_t head_dim, int64_t n_blocks, int64_t block_size,
+                     int64_t group, int64_t super_slots, int64_t slots, int64_t take,
+                     int always_current, int dtype, void* stream);
+
+/*
  * moba_gate without a workspace argument, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference.

@@ -790,6 +790,73 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 }
 
 // ---------------------------------------------------------------------------
+// Hierarchical refinement (opt-in): one wave per query. The candidates are
+// the strictly-past blocks inside the super-blocks the super-block gate
+// opened for the query (`sup`: ascending super-block ids, -1 padded, the
+// query's own super-block among them); each lane scores up to LMAX of them
+// exactly, keeps them sorted by (score desc, id asc), and `take` rounds of a
+// wave-wide arg-max pick the best. Scores follow the gate's definition:
+// the exact dot product rounded to float32 and to the input dtype.
+// ---------------------------------------------------------------------------
+template <typename T, int LMAX, int TMAX>
+__global__ void __launch_bounds__(256)
+gate_refine_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
+                   const int32_t* __restrict__ sup, int32_t* __restrict__ out,
+                   int64_t S, int64_t h_q, int64_t h_kv, int D, int64_t n_blocks, int bs,
+                   int group, int sup_slots, int take, int cur, int slots) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rh = blockIdx.y;
+  const int64_t r = rh / h_q, hq = rh % h_q;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= S) return;  // uniform over the wave
+  const int own = static_cast<int>(t / bs);
+  const T* qrow = q + ((r * S + t) * h_q + hq) * D;
+  const T* kb = kbar + (r * h_kv + hq / (h_q / h_kv)) * n_blocks * D;
+  const int32_t* sp = sup + (rh * S + t) * sup_slots;
+  float val[LMAX];
+  int idx[LMAX];
+#pragma unroll
+  for (int p = 0; p < LMAX; ++p) { val[p] = -INFINITY; idx[p] = 0x7fffffff; }
+  const int n_cand = sup_slots * group;
+#pragma unroll
+  for (int u = 0; u < LMAX; ++u) {
+    const int c = lane + 64 * u;
+    if (c >= n_cand) break;
+    const int sb = sp[c / group];
+    const int j = sb * group + c % group;
+    if (sb < 0 || j >= own || j >= n_blocks) continue;
+    insert_exact<LMAX>(val, idx, exact_score(qrow, kb + static_cast<int64_t>(j) * D, D), j);
+  }
+  int sel[TMAX];
+  int n_sel = 0;
+  for (int round = 0; round < take; ++round) {
+    // Wave-wide best of the lanes' heads under (score desc, id asc).
+    float bv = val[0];
+    int bi = idx[0];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const int oi = __shfl_xor(bi, off);
+      if (ranks_before(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (!(bv > -INFINITY)) break;  // no candidate left (uniform)
+    if (idx[0] == bi) {            // the owner drops its head
+#pragma unroll
+      for (int p = 0; p + 1 < LMAX; ++p) { val[p] = val[p + 1]; idx[p] = idx[p + 1]; }
+      val[LMAX - 1] = -INFINITY;
+      idx[LMAX - 1] = 0x7fffffff;
+    }
+#pragma unroll
+    for (int p = 0; p < TMAX; ++p) if (p == n_sel) sel[p] = bi;
+    ++n_sel;
+  }
+  if (lane != 0) return;
+#pragma unroll
+  for (int p = 0; p < TMAX; ++p) if (p >= n_sel) sel[p] = 0x7fffffff;
+  emit_sorted<TMAX>(sel, n_sel, own, cur != 0, out + (rh * S + t) * slots, slots);
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------
 template <typename T, int TMAX>
@@ -1007,5 +1074,69 @@ extern "C" int moba_gate(const void* q, const void* kbar, int32_t* block_idx,
     return run_gate<T>(q, kbar, block_idx, cu_seqlens, g, static_cast<int>(take),
                        always_current ? 1 : 0, workspace, workspace_bytes,
                        as_stream(stream));
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Hierarchical gate, second stage (opt-in).
+// ---------------------------------------------------------------------------
+namespace moba {
+
+template <typename T>
+static int launch_refine(const void* q, const void* kbar, const int32_t* sup, int32_t* out,
+                         const Geometry& g, int group, int sup_slots, int take, int cur,
+                         hipStream_t st) {
+  const int n_cand = sup_slots * group;
+  dim3 grid(static_cast<unsigned>(cdiv(g.seq_len, 4)), static_cast<unsigned>(g.rows * g.h_q));
+  const int D = static_cast<int>(g.head_dim), bs = static_cast<int>(g.block_size);
+  const int slots = static_cast<int>(g.slots);
+#define MOBA_REFINE(L, TM)                                                                 \
+  hipLaunchKernelGGL((gate_refine_kernel<T, L, TM>), grid, dim3(256), 0, st,              \
+                     static_cast<const T*>(q), static_cast<const T*>(kbar), sup, out,      \
+                     g.seq_len, g.h_q, g.h_kv, D, g.n_blocks, bs, group, sup_slots, take,  \
+                     cur, slots)
+  if (take > 16) return fail(MOBA_ERR_UNSUPPORTED, "moba_gate_refine: at most 16 past blocks");
+  if (n_cand <= 64) {
+    MOBA_REFINE(1, 16);
+  } else if (n_cand <= 128) {
+    MOBA_REFINE(2, 16);
+  } else if (n_cand <= 256) {
+    MOBA_REFINE(4, 16);
+  } else if (n_cand <= 512) {
+    MOBA_REFINE(8, 16);
+  } else {
+    return fail(MOBA_ERR_UNSUPPORTED,
+                "moba_gate_refine: (opened + 1) * group must be at most 512 candidates");
+  }
+#undef MOBA_REFINE
+  return check_launch("moba_gate_refine");
+}
+
+}  // namespace moba
+
+extern "C" int moba_gate_refine(const void* q, const void* kbar, const int32_t* super_idx,
+                                int32_t* block_idx, int64_t batch, int64_t seq_len,
+                                int64_t h_q, int64_t h_kv, int64_t head_dim, int64_t n_blocks,
+                                int64_t block_size, int64_t group, int64_t super_slots,
+                                int64_t slots, int64_t take, int always_current, int dtype,
+                                void* stream) {
+  using namespace moba;
+  Geometry g;
+  int st = make_geometry(&g, batch, seq_len, seq_len, h_q, h_kv, head_dim, n_blocks,
+                         block_size, slots, nullptr);
+  if (st) return st;
+  if (!q || !kbar || !super_idx || !block_idx) return fail(MOBA_ERR_INVALID, "null pointer");
+  if (group <= 0 || super_slots <= 0)
+    return fail(MOBA_ERR_INVALID, "moba_gate_refine: group and super_slots must be positive");
+  if (take < 0 || slots < take + (always_current ? 1 : 0))
+    return fail(MOBA_ERR_INVALID, "slots must hold take (+1 with the own block)");
+  if (super_slots * group > 512)
+    return fail(MOBA_ERR_UNSUPPORTED,
+                "moba_gate_refine: super_slots * group must be at most 512 candidates");
+  if (head_dim % 8 != 0) return fail(MOBA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
+  return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
+    return launch_refine<T>(q, kbar, super_idx, block_idx, g, static_cast<int>(group),
+                            static_cast<int>(super_slots), static_cast<int>(take),
+                            always_current ? 1 : 0, as_stream(stream));
   });
 }

@@ -34,6 +34,8 @@ SIGNATURES = {
     "moba_gate_workspace_size": (_Z, [_L, _L, _L]),
     "moba_gate": (_I, [_P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
                        _I, _I, _P, _Z, _P]),
+    "moba_gate_refine": (_I, [_P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
+                              _I, _I, _P]),
     "moba_gate_noalloc": (_I, [_P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L,
                                _I, _I, _P]),
     "moba_csc_workspace_size": (_Z, [_L, _L, _L, _L, _L, _L]),

@@ -30,6 +30,15 @@ class MoBAConfig:
             unspecified).
         pool_masked_only: Carried for compatibility; the reference's pooling
             averages the whole block regardless (`naive.py:23-61`).
+        gate_group: Opt-in hierarchical gate (0, the default, is the exact
+            gate): blocks grouped into super-blocks of `gate_group`, whose
+            representatives (the mean of their blocks' representatives)
+            are gated first; only blocks inside the `gate_open` best
+            strictly-past super-blocks and the query's own super-block are
+            then ranked. An approximation of the exact selection (the
+            reference measured it, `docs/gate-hierarchical-measurements.md`,
+            and built no kernel): it changes which blocks are selected.
+        gate_open: Super-blocks opened per query when `gate_group` > 0.
     """
 
     block_size: int
@@ -39,12 +48,18 @@ class MoBAConfig:
     top_k_includes_current: bool = True
     tie_break_low_index: bool = True
     pool_masked_only: bool = False
+    gate_group: int = 0
+    gate_open: int = 0
 
     def __post_init__(self) -> None:
         if self.block_size <= 0:
             raise ValueError(f"block_size must be positive, got {self.block_size}")
         if self.top_k <= 0:
             raise ValueError(f"top_k must be positive, got {self.top_k}")
+        if self.gate_group < 0 or self.gate_open < 0:
+            raise ValueError("gate_group and gate_open must be non-negative")
+        if self.gate_group > 0 and self.gate_open <= 0:
+            raise ValueError("gate_open must be positive when gate_group is set")
 
     def past_blocks_selected(self, num_blocks: int) -> int:
         """Past-block budget per query, clamped to [0, num_blocks]

@@ -20,6 +20,7 @@ __all__ = [
     "gate_select", "moba_selection", "mask_to_indices", "indices_to_mask",
     "moba_attention", "moba_attention_sparse", "build_csc", "csc_to_mask",
     "combine_reference", "slots_per_query", "sparse_grads",
+    "super_block_means", "hierarchical_select",
 ]
 
 
@@ -183,6 +184,51 @@ def gate_select_rows(q: torch.Tensor, kbar: torch.Tensor, cfg, rows) -> torch.Te
     the dense `[S, n]` score matrix would not fit."""
     rows = torch.as_tensor(rows, dtype=torch.int64)
     return select_from_scores(gate_scores(q[:, rows], kbar), cfg, pos=rows)
+
+
+def super_block_means(kbar: torch.Tensor, group: int) -> torch.Tensor:
+    """Super-block representatives `[B, H, ceil(n / group), D]`: the blocks'
+    representatives pooled `group` at a time exactly as `pool_blocks` pools
+    keys (sum rounded to the dtype, divided by the real count, a short tail
+    by its own). This build's definition for the opt-in hierarchical gate;
+    the reference's probe pooled the same way in spirit
+    (`docs/gate-hierarchical-measurements.md`, "mean-pooled super-block
+    representatives")."""
+    return pool_blocks(kbar.transpose(1, 2), group)
+
+
+def hierarchical_select(q: torch.Tensor, kbar: torch.Tensor, cfg, group: int,
+                        opened: int, rows=None) -> torch.Tensor:
+    """Coarse-to-fine selection mask `[B, H, S, n]` (opt-in; never the
+    default). Restates the scheme of `docs/gate-hierarchical-measurements.md`
+    (group blocks into super-blocks of `group`, score the super-block
+    representatives, open the best `opened`, score only the blocks inside):
+
+    1. the super-block gate: `gate_select` over `super_block_means(kbar,
+       group)` with block size `block_size * group`, `opened` strictly-past
+       super-blocks plus the query's own super-block;
+    2. candidates: the strictly-past blocks inside those super-blocks;
+    3. the usual ranking (`select_from_scores`: exact score rounded to
+       float32 and to the dtype, ties to the lower block) over the
+       candidates only; the own block forced as usual.
+    With `opened` >= the number of super-blocks, or `group` 1 and `opened` >=
+    the past budget, this is `gate_select` exactly. `rows` restricts the
+    result to those query positions (`[B, H, len(rows), n]`), as
+    `gate_select_rows` does.
+    """
+    from types import SimpleNamespace
+    n = kbar.shape[2]
+    pos = torch.arange(q.shape[1]) if rows is None else torch.as_tensor(rows, dtype=torch.int64)
+    qr = q if rows is None else q[:, pos]
+    scfg = SimpleNamespace(block_size=cfg.block_size * group, top_k=opened + 1,
+                           always_select_current=True, top_k_includes_current=True,
+                           tie_break_low_index=True)
+    sup = select_from_scores(gate_scores(qr, super_block_means(kbar, group)), scfg, pos=pos)
+    cand = sup[..., torch.arange(n) // group]                         # [B, H, R, n]
+    scores = gate_scores(qr, kbar).masked_fill(~cand, float("-inf"))
+    sel = select_from_scores(scores, cfg, pos=pos)
+    own = (pos // cfg.block_size).view(1, 1, -1, 1)
+    return sel & (cand | (torch.arange(n).view(1, 1, 1, n) == own))
 
 
 def moba_selection(q, k, cfg, cu_seqlens=None) -> torch.Tensor:

@@ -171,3 +171,13 @@ def test_chunk_plan_sizes_packed_units_by_total_tokens():
     assert plan_call((1, t, h, d), h, slots, 4, budget=unit + unit // 2) == \
         [(0, 1, hk, hk + 1, 0, 1) for hk in range(h)]
     assert len(plan_call((1, t, h, d), h, slots, 4, budget=2 * unit)) == 4
+
+
+def test_hierarchical_gate_config_fields():
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    assert cfg.gate_group == 0 and cfg.gate_open == 0  # exact gate by default
+    MoBAConfig(block_size=128, top_k=8, gate_group=16, gate_open=8)
+    with pytest.raises(ValueError, match="gate_open"):
+        MoBAConfig(block_size=128, top_k=8, gate_group=16)
+    with pytest.raises(ValueError, match="non-negative"):
+        MoBAConfig(block_size=128, top_k=8, gate_group=-1, gate_open=2)

@@ -284,3 +284,67 @@ def test_hand_gradients_in_bfloat16_track_float64():
         assert a.dtype is torch.bfloat16
         err = (a.double() - b).abs().max().item()
         assert 1e-5 < err < 5e-2 * max(1.0, b.abs().max().item()), err
+
+
+def _brute_hierarchical(q, k, bs, tk, group, opened):
+    """Per query, in plain loops: super-block scores of the representatives'
+    means, the best `opened` past super-blocks, then the best past blocks
+    inside them (and inside the own super-block) by (score desc, id asc)."""
+    b, s, h, d = q.shape
+    kbar = O.pool_blocks(k, bs)
+    n = kbar.shape[2]
+    sbar = O.super_block_means(kbar, group)
+    take = min(tk - 1, n)
+    out = torch.zeros(b, h, s, n, dtype=torch.bool)
+    for bi in range(b):
+        for hi in range(h):
+            for t in range(s):
+                own = t // bs
+                own_sb = t // (bs * group)
+                sups = sorted(range(own_sb), key=lambda x: (-float(O.round_to_dtype(
+                    (q[bi, t, hi].double() * sbar[bi, hi, x].double()).sum(), q.dtype)), x))
+                opened_set = set(sups[:opened]) | {own_sb}
+                cands = [j for j in range(own) if j // group in opened_set]
+                ranked = sorted(cands, key=lambda j: (-float(O.round_to_dtype(
+                    (q[bi, t, hi].double() * kbar[bi, hi, j].double()).sum(), q.dtype)), j))
+                for j in ranked[:take]:
+                    out[bi, hi, t, j] = True
+                out[bi, hi, t, own] = True
+    return out
+
+
+@pytest.mark.parametrize("s,bs,tk,group,opened", [(256, 8, 4, 4, 2), (300, 16, 3, 2, 1),
+                                                 (512, 8, 5, 8, 3)])
+def test_hierarchical_gate_equals_brute_force(s, bs, tk, group, opened):
+    q, k, _ = qkv(1, s, 2, 16, seed=12)
+    c = cfg(bs, tk)
+    got = O.hierarchical_select(q, O.pool_blocks(k, bs), c, group, opened)
+    assert torch.equal(got, _brute_hierarchical(q, k, bs, tk, group, opened))
+
+
+@pytest.mark.parametrize("dt", [torch.float64, torch.bfloat16])
+def test_hierarchical_gate_reduces_to_the_exact_gate(dt):
+    """Opening every super-block, or super-blocks of one block opened as many
+    as the past budget, leaves the exact gate."""
+    q, k, _ = qkv(1, 1024, 2, 32, seed=13)
+    q, k = q.to(dt), k.to(dt)
+    c = cfg(16, 6)
+    kbar = O.pool_blocks(k, 16)
+    exact = O.gate_select(q, kbar, c)
+    assert torch.equal(O.hierarchical_select(q, kbar, c, 4, 1024 // 64), exact)
+    assert torch.equal(O.hierarchical_select(q, kbar, c, 1, 5), exact)
+    # A real restriction changes some selections and never the own block.
+    h = O.hierarchical_select(q, kbar, c, 4, 1)
+    assert not torch.equal(h, exact)
+    own = (torch.arange(1024) // 16)
+    assert bool(h[0, :, torch.arange(1024), own].all())
+    assert int(h.sum(-1).max()) <= 6
+
+
+def test_hierarchical_gate_rows_equal_the_full_result_restricted():
+    q, k, _ = qkv(1, 700, 2, 16, seed=14)
+    c = cfg(16, 4)
+    kbar = O.pool_blocks(k, 16)
+    rows = torch.tensor([0, 15, 16, 200, 511, 699])
+    full = O.hierarchical_select(q, kbar, c, 4, 2)
+    assert torch.equal(O.hierarchical_select(q, kbar, c, 4, 2, rows=rows), full[:, :, rows])
