@@ -2,8 +2,8 @@
 //
 // This file holds the C ABI entry points of the attention stages and the
 // general kernels behind them: every dtype (the float32 path always runs
-// here), any power-of-two head_dim up to 128 with block_size * head_dim <=
-// 16384. The bf16 / fp16 MFMA kernels (attn_mfma.hip) take the shapes they
+// here), any head_dim from 8 to 256 (a multiple of 8) whose block of keys
+// and values fits in LDS at the input's width. The bf16 / fp16 MFMA kernels (attn_mfma.hip) take the shapes they
 // cover and report MOBA_ERR_UNSUPPORTED otherwise, which routes here.
 //
 // Semantics restated:
@@ -40,9 +40,11 @@ __global__ void __launch_bounds__(256)
 attend_simple_kernel(AttnArgs a) {
   extern __shared__ float smem[];
   const int64_t D = a.D, bs = a.bs;
-  float* Ks = smem;                 // [bs][D]
-  float* Vs = Ks + bs * D;          // [bs][D]
-  float* Qs = Vs + bs * D;          // [kE][D]
+  // The block's keys and values stay in the input type (16-bit types take
+  // half the LDS, so a 128-key block of head_dim 256 fits).
+  T* Ks = reinterpret_cast<T*>(smem);  // [bs][D]
+  T* Vs = Ks + bs * D;                 // [bs][D]
+  float* Qs = reinterpret_cast<float*>(Vs + bs * D);  // [kE][D]
   float* Ss = Qs + kE * D;          // [kE][bs]
   float* Ms = Ss + kE * bs;         // [kE]
   float* Ls = Ms + kE;              // [kE]
@@ -59,8 +61,8 @@ attend_simple_kernel(AttnArgs a) {
     const int64_t j = i / D, d = i % D;
     const bool ok = c.key0 + j < c.key_end;
     const int64_t off = ((c.tok0 + j) * a.h_kv + c.hk) * D + d;
-    Ks[i] = ok ? Elem<T>::load(K, off) : 0.f;
-    Vs[i] = ok ? Elem<T>::load(V, off) : 0.f;
+    Ks[i] = ok ? K[off] : T{};
+    Vs[i] = ok ? V[off] : T{};
   }
   for (int32_t e0 = 0; e0 < c.n; e0 += kE) {
     __syncthreads();
@@ -83,7 +85,7 @@ attend_simple_kernel(AttnArgs a) {
       const int64_t j = i % bs;
       const int64_t kpos = c.key0 + j;
       float s = 0.f;
-      for (int64_t d = 0; d < D; ++d) s = fmaf(Qs[e * D + d], Ks[j * D + d], s);
+      for (int64_t d = 0; d < D; ++d) s = fmaf(Qs[e * D + d], Elem<T>::load(Ks, j * D + d), s);
       s *= a.scale_log2;
       const bool ok = kpos < c.key_end && (!a.causal || kpos <= Rs[e]);
       Ss[i] = ok ? s : neg_inf();
@@ -113,7 +115,7 @@ attend_simple_kernel(AttnArgs a) {
       const int64_t d = i % D;
       if (Rs[e] < 0) continue;
       float acc = 0.f;
-      for (int64_t j = 0; j < bs; ++j) acc = fmaf(Ss[e * bs + j], Vs[j * D + d], acc);
+      for (int64_t j = 0; j < bs; ++j) acc = fmaf(Ss[e * bs + j], Elem<T>::load(Vs, j * D + d), acc);
       const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
       Elem<A>::store(acc_out, dst * D + d, acc);
     }
@@ -123,7 +125,7 @@ attend_simple_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Backward: dK / dV per key tile, one program per (column, key tile).
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int MAXD>
 __global__ void __launch_bounds__(256)
 bwd_dkdv_simple_kernel(AttnArgs a) {
   extern __shared__ float smem[];
@@ -158,7 +160,7 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
   // float32 path accumulates in float64 so the sum's rounding stays far
   // below its 1e-5 bar; the 16-bit paths round to 8 or 11 bits anyway.
   using Acc = typename std::conditional<sizeof(T) == 4, double, float>::type;
-  constexpr int kMaxOwn = (kKT * 128) / 256;
+  constexpr int kMaxOwn = (kKT * MAXD) / 256;
   Acc dk[kMaxOwn], dv[kMaxOwn];
 #pragma unroll
   for (int u = 0; u < kMaxOwn; ++u) { dk[u] = 0; dv[u] = 0; }
@@ -228,7 +230,7 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Backward: per-slot dQ partials, one program per column.
 // ---------------------------------------------------------------------------
-template <typename T, typename A>
+template <typename T, typename A, int MAXD>
 __global__ void __launch_bounds__(256)
 bwd_dq_simple_kernel(AttnArgs a) {
   extern __shared__ float smem[];
@@ -251,7 +253,7 @@ bwd_dq_simple_kernel(AttnArgs a) {
   const T* Q = static_cast<const T*>(a.q);
   const T* dO = static_cast<const T*>(a.dout);
   A* out = static_cast<A*>(a.part_acc);
-  constexpr int kMaxOwn = (kE * 128) / 256;
+  constexpr int kMaxOwn = (kE * MAXD) / 256;
   const int own = static_cast<int>((kE * D) / 256);
   for (int32_t e0 = 0; e0 < c.n; e0 += kE) {
     __syncthreads();
@@ -605,8 +607,10 @@ static int set_segments(AttnArgs* a, const int32_t* segments, const int32_t* seg
   return MOBA_OK;
 }
 
+// The FMA kernels take head_dim 8..256; the attend kernel keeps a block's
+// keys and values in LDS at the input's width.
 static bool simple_shape_ok(const Geometry& g) {
-  return g.head_dim <= 128 && g.head_dim >= 8 && g.block_size * g.head_dim <= 16384;
+  return g.head_dim <= 256 && g.head_dim >= 8;
 }
 
 template <typename K>
@@ -669,9 +673,15 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
   if (st != MOBA_ERR_UNSUPPORTED) return st;
   a.seg = nullptr;  // the FMA kernels take whole columns
   if (!simple_shape_ok(g))
-    return fail(MOBA_ERR_UNSUPPORTED, "attend: block_size * head_dim must be <= 16384");
-  const size_t lds = sizeof(float) * (2 * block_size * head_dim + kE * head_dim +
-                                      kE * block_size + 2 * kE) + sizeof(int) * 3 * kE;
+    return fail(MOBA_ERR_UNSUPPORTED, "attend: head_dim must be in [8, 256]");
+  const size_t esize = dtype == MOBA_FP32 ? 4 : 2;
+  const size_t lds = esize * 2 * block_size * head_dim +
+                     sizeof(float) * (kE * head_dim + kE * block_size + 2 * kE) +
+                     sizeof(int) * 3 * kE;
+  if (lds > 160 * 1024)
+    return fail(MOBA_ERR_UNSUPPORTED,
+                "attend: a block's keys and values must fit in LDS (2 * block_size * "
+                "head_dim * element bytes <= about 130000)");
   dim3 grid(static_cast<unsigned>(n_blocks), static_cast<unsigned>(batch * h_kv));
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
     return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
@@ -783,8 +793,8 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
   }
   if (st != MOBA_ERR_UNSUPPORTED) return st;
   a.seg = nullptr;  // the FMA kernels take whole columns
-  if (head_dim > 128 || head_dim < 8)
-    return fail(MOBA_ERR_UNSUPPORTED, "backward: head_dim must be in [8, 128]");
+  if (head_dim > 256 || head_dim < 8)
+    return fail(MOBA_ERR_UNSUPPORTED, "backward: head_dim must be in [8, 256]");
   const int64_t tiles = cdiv(block_size, kKT);
   const size_t lds_kv = sizeof(float) * (2 * kKT * head_dim + 2 * kBE * head_dim +
                                          2 * kBE * kKT + 2 * kBE) + sizeof(int) * 2 * kBE;
@@ -792,20 +802,25 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
                                         kE * kKT + 2 * kE) + sizeof(int) * 3 * kE;
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
     return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
-      int rc = set_lds(bwd_dkdv_simple_kernel<T>, lds_kv);
-      if (rc) return rc;
-      rc = set_lds(bwd_dq_simple_kernel<T, A>, lds_q);
-      if (rc) return rc;
-      hipLaunchKernelGGL(bwd_dkdv_simple_kernel<T>,
-                         dim3(static_cast<unsigned>(n_blocks * tiles),
-                              static_cast<unsigned>(batch * h_kv)),
-                         dim3(256), lds_kv, s, a);
-      rc = check_launch("moba_bwd (dk/dv)");
-      if (rc) return rc;
-      hipLaunchKernelGGL((bwd_dq_simple_kernel<T, A>),
-                         dim3(static_cast<unsigned>(n_blocks), static_cast<unsigned>(batch * h_kv)),
-                         dim3(256), lds_q, s, a);
-      return check_launch("moba_bwd (dq)");
+      auto run = [&](auto dkdv_kernel, auto dq_kernel) {
+        int rc = set_lds(dkdv_kernel, lds_kv);
+        if (rc) return rc;
+        rc = set_lds(dq_kernel, lds_q);
+        if (rc) return rc;
+        hipLaunchKernelGGL(dkdv_kernel,
+                           dim3(static_cast<unsigned>(n_blocks * tiles),
+                                static_cast<unsigned>(batch * h_kv)),
+                           dim3(256), lds_kv, s, a);
+        rc = check_launch("moba_bwd (dk/dv)");
+        if (rc) return rc;
+        hipLaunchKernelGGL(dq_kernel,
+                           dim3(static_cast<unsigned>(n_blocks), static_cast<unsigned>(batch * h_kv)),
+                           dim3(256), lds_q, s, a);
+        return check_launch("moba_bwd (dq)");
+      };
+      if (head_dim <= 128)
+        return run(bwd_dkdv_simple_kernel<T, 128>, bwd_dq_simple_kernel<T, A, 128>);
+      return run(bwd_dkdv_simple_kernel<T, 256>, bwd_dq_simple_kernel<T, A, 256>);
     });
   });
 }

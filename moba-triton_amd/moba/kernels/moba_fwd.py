@@ -152,8 +152,10 @@ def _validate(q, k, v, cfg: MoBAConfig, cu_seqlens=None, max_seqlen=None) -> Non
     ok, reason = check_gathered_head_dim(q.shape[-1], q.element_size())
     if not ok:
         raise ValueError(reason)
-    if q.shape[-1] > 128:
-        raise ValueError(f"head_dim {q.shape[-1]} above 128 is not supported")
+    if q.shape[-1] > 256:
+        # The reference admits any power of two (moba_fwd.py:774-776); the
+        # kernels here cover up to 256 (MFMA at 64 and 128, FMA beyond).
+        raise ValueError(f"head_dim {q.shape[-1]} above 256 is not supported")
     if cfg.block_size < TENSOR_CORE_TILE:
         raise ValueError(f"block_size {cfg.block_size} below the MFMA tile minimum "
                          f"of {TENSOR_CORE_TILE}")

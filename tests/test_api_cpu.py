@@ -181,3 +181,12 @@ def test_hierarchical_gate_config_fields():
         MoBAConfig(block_size=128, top_k=8, gate_group=16)
     with pytest.raises(ValueError, match="non-negative"):
         MoBAConfig(block_size=128, top_k=8, gate_group=-1, gate_open=2)
+
+
+def test_validation_head_dim_range():
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    z = torch.zeros(1, 256, 2, 256, dtype=torch.bfloat16)
+    _validate(z, z, z, cfg)  # head_dim 256 is accepted (FMA kernels)
+    with pytest.raises(ValueError, match="above 256"):
+        z = torch.zeros(1, 256, 2, 512, dtype=torch.bfloat16)
+        _validate(z, z, z, cfg)

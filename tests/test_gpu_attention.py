@@ -410,3 +410,34 @@ def test_cut_columns_equal_whole_columns(device, monkeypatch, shape, h_kv, cu):
         assert mean_abs_error(a.float(), b.float()) <= BF16_MEAN_ABS
     again = run(cut[0])  # repeatable given the index (its column order is not fixed)
     assert torch.equal(cut[3], again[3]) and torch.equal(cut[4], again[4])
+
+
+@pytest.mark.parametrize("dtype,bs", [(torch.bfloat16, 128), (torch.float16, 64),
+                                      (torch.float32, 64)])
+def test_head_dim_256_forward_and_backward(device, dtype, bs):
+    """head_dim 256 (admitted by the reference's _validate, moba_fwd.py:774-776)
+    runs on the FMA kernels: forward and gradients against fp64 autograd of
+    the oracle, under the dtype's bar."""
+    cfg = MoBAConfig(block_size=bs, top_k=4, dtype=dtype)
+    shape = (1, 1024, 2, 256)
+    q, k, v = make_qkv(shape, dtype, seed=31, device=device)
+    g = make_qkv(shape, dtype, seed=32, device=device, n=1)[0]
+    sel = oracle_selection(q, k, cfg)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = moba_attention(qq, kk, vv, cfg)
+    out.backward(g)
+    qc, kc, vc, gc = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v, g))
+    ref = O.moba_attention(qc, kc, vc, oracle_cfg(cfg), selected=sel, query_chunk=256)
+    ref.backward(gc.detach())
+    if dtype == torch.float32:
+        for name, ours, tr in (("out", out, ref), ("dq", qq.grad, qc.grad),
+                               ("dk", kk.grad, kc.grad), ("dv", vv.grad, vc.grad)):
+            assert max_abs_error(ours, tr) <= FP32_MAX_ABS, name
+        return
+    low = grads_oracle(q, k, v, cfg, sel, g, dtype=dtype)
+    lo_out = O.moba_attention(*(t.detach().cpu().to(dtype) for t in (q, k, v)), oracle_cfg(cfg),
+                              selected=sel, query_chunk=256)
+    for name, ours, tr, lo in (("out", out, ref, lo_out), ("dq", qq.grad, qc.grad, low[0]),
+                               ("dk", kk.grad, kc.grad, low[1]), ("dv", vv.grad, vc.grad, low[2])):
+        assert_within_tolerance(ours, tr, max_abs_error(lo, tr), name)
+        assert mean_abs_error(ours, tr) <= BF16_MEAN_ABS, name
