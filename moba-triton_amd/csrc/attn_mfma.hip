@@ -416,7 +416,10 @@ bwd_mfma_kernel(AttnArgs a) {
   constexpr int DT = D / 32;
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
   constexpr int KTS = BS + 8;   // row stride of K^T ([d][key])
-  constexpr int QS2 = NQ + 8;   // row stride of dS^T ([key][q])
+  // Row stride of dS^T ([key][q]): 34 banks, so the 32 keys of a wave's
+  // 8-byte dS writes land on distinct bank pairs (NQ + 8 paired keys c and
+  // c + 16; measured 2% faster at 512K).
+  constexpr int QS2 = NQ + 4;
   __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
   __shared__ __attribute__((aligned(16))) uint16_t Qs[NQ * RS];
   __shared__ __attribute__((aligned(16))) uint16_t Os[NQ * RS];
