@@ -211,6 +211,52 @@ def stage_times(s, dev, reps=5):
     return st
 
 
+def other_configs(dev, reps=5):
+    """BASELINE.json configs 4 and 5 (config 3 is the sweep's 128K row):
+    fwd and fwd+bwd device time of `moba_attention`, bf16, block 128, top-k 8.
+    Config 4: GQA S=32768, Hq=32, Hkv=8, D=128. Config 5: 8 sequences of
+    lengths U[2048, 131072] (seeded), rounded down to multiples of 128,
+    packed (~512K tokens), H=4, D=64."""
+    from moba.config import MoBAConfig
+    from moba.kernels.attention import moba_attention
+    from moba.kernels.moba_fwd import moba_forward
+
+    cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
+    out = []
+    g = torch.Generator().manual_seed(0)
+    lens = [int(x) // BLOCK * BLOCK for x in torch.randint(2048, 131073, (8,), generator=g)]
+    cases = [("config4_gqa", (1, 32768, 32, 128), 8, None),
+             ("config5_varlen", (1, sum(lens), 4, 64), 4, lens)]
+    for name, (b, s, hq, d), hkv, ln in cases:
+        gd = torch.Generator(device=dev).manual_seed(0)
+        q = torch.randn((b, s, hq, d), generator=gd, device=dev, dtype=torch.bfloat16)
+        k, v = (torch.randn((b, s, hkv, d), generator=gd, device=dev, dtype=torch.bfloat16)
+                for _ in range(2))
+        do = torch.randn_like(q)
+        kw = {}
+        if ln is not None:
+            cu = torch.tensor([0] + torch.cumsum(torch.tensor(ln), 0).tolist(), dtype=torch.int32,
+                              device=dev)
+            kw = {"cu_seqlens": cu, "max_seqlen": max(ln)}
+        fwd = timed(lambda: moba_forward(q, k, v, cfg, **kw), reps, 2)[0]
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+        def step():
+            qq.grad = kk.grad = vv.grad = None
+            moba_attention(qq, kk, vv, cfg, **kw).backward(do)
+
+        fb = timed(step, reps, 2)[0]
+        row = {"config": name, "shape": [b, s, hq, d], "heads_kv": hkv,
+               "fwd_ms": round(fwd, 4), "fwd_bwd_ms": round(fb, 4),
+               "tokens_per_s_fwd_bwd": round(s / (fb * 1e-3), 1)}
+        if ln is not None:
+            row["seq_lens"] = ln
+        out.append(row)
+        del q, k, v, do, qq, kk, vv
+        torch.cuda.empty_cache()
+    return out
+
+
 def hierarchical_gate(s, dev, configs=((16, 8), (4, 8)), reps=5):
     """The opt-in hierarchical gate (`MoBAConfig.gate_group` / `gate_open`)
     beside the exact gate at S: device time of `gate_select` and recall --
@@ -452,6 +498,8 @@ def main():
     rows = [] if args.no_sweep else sweep(dev, SWEEP)
     hier = None if args.no_hier else hierarchical_gate(s, dev)
     torch.cuda.empty_cache()
+    configs = [] if args.no_sweep else other_configs(dev)
+    torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline(s, args.cpu_rows)
     tokens = s  # query tokens per step (batch 1)
     line = {
@@ -472,6 +520,7 @@ def main():
         "stages": stage_rows,
         "sweep": rows,
         "hierarchical_gate": hier,
+        "other_configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
