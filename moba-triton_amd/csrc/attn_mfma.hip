@@ -1,7 +1,7 @@
 // bf16 / fp16 MFMA kernels of the KV-block-major attention (gfx950).
 //
 // Forward (attend_mfma_kernel): one workgroup per (KV block, row * kv head),
-// four waves. The block's K (row-major) and V (transposed, key order
+// four waves (eight when one workgroup fills a CU's LDS). The block's K (row-major) and V (transposed, key order
 // permuted per 16-key slice) are staged once in LDS. Each wave then takes
 // groups of 32 column entries and runs, with v_mfma_f32_32x32x16:
 //
@@ -18,7 +18,8 @@
 //
 // Semantics: src/moba/kernels/moba_fwd.py:230-425 -- additive tail / causal
 // masks, m = max(q.k * D^-1/2 * log2 e), p = exp2(s - m) rounded to the
-// input dtype for the PV product, l = sum p (float32), partials stored at the
+// input dtype for the PV product, l = sum p (float32; at head_dim >= 128
+// the sum of the rounded p, on the matrix cores), partials stored at the
 // query's fixed slot.
 #include <type_traits>
 
@@ -99,8 +100,14 @@ __device__ inline void store4<float>(float* p, float x0, float x1, float x2, flo
 // lane-half h = bit 2 of o owns positions [8h, 8h + 8).
 __device__ inline int perm16(int o) { return ((o >> 2) & 1) * 8 + (o >> 3) * 4 + (o & 3); }
 
+// Waves per attend workgroup. Each wave works through its own 32-entry
+// groups, so the count only sets how many waves share one K / V^T tile: 4
+// where two workgroups fit a CU's LDS, 8 where one workgroup fills it (so
+// a CU still runs 2 waves per SIMD).
+__host__ __device__ constexpr int attend_waves(int D, int BS) { return D * BS > 8192 ? 8 : 4; }
+
 template <typename T, typename A, int D, int BS>
-__global__ void __launch_bounds__(256, (D * BS > 8192) ? 1 : 2)
+__global__ void __launch_bounds__(64 * attend_waves(D, BS), (D * BS > 8192) ? 1 : 2)
 attend_mfma_kernel(AttnArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec;
@@ -118,7 +125,9 @@ attend_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[BS * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
   // Per wave: the group's Q rows on the way in, its partial rows on the way out.
-  __shared__ __attribute__((aligned(16))) uint16_t Rw[4][32 * KS];
+  constexpr int NWV = attend_waves(D, BS);
+  constexpr int NT = 64 * NWV;
+  __shared__ __attribute__((aligned(16))) uint16_t Rw[NWV][32 * KS];
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
   if (c.n == 0) return;
@@ -164,14 +173,14 @@ attend_mfma_kernel(AttnArgs a) {
   // the block are requested together, the first group's Q rows as soon as
   // its entries are in, and only then are K and V^T (permuted keys) written
   // to LDS -- one memory round trip before the first group, not several.
-  constexpr int KVN = BS * D / 8 / 256;  // 16-byte K (and V) chunks per thread
-  static_assert(BS * D / 8 % 256 == 0, "K / V chunks must tile the workgroup");
+  constexpr int KVN = BS * D / 8 / NT;  // 16-byte K (and V) chunks per thread
+  static_assert(BS * D / 8 % NT == 0, "K / V chunks must tile the workgroup");
   int32_t cr, chd, csl, nr, nhd, nsl;
   load_idx(wave * 32, cr, chd, csl);
   u32x4 kc[KVN], vc[KVN];
 #pragma unroll
   for (int u = 0; u < KVN; ++u) {
-    const int i = tid + u * 256;
+    const int i = tid + u * NT;
     const int key = i / (D / 8);
     const int d8 = (i % (D / 8)) * 8;
     const int kk = c.key0 + key < c.key_end ? key : 0;  // tail keys: a valid row, zeroed below
@@ -180,10 +189,10 @@ attend_mfma_kernel(AttnArgs a) {
     vc[u] = *reinterpret_cast<const u32x4*>(Vg + off);
   }
   fetch(q_off(cr, chd, csl));
-  load_idx(wave * 32 + 128, nr, nhd, nsl);
+  load_idx(wave * 32 + NWV * 32, nr, nhd, nsl);
 #pragma unroll
   for (int u = 0; u < KVN; ++u) {
-    const int i = tid + u * 256;
+    const int i = tid + u * NT;
     const int key = i / (D / 8);
     const int d8 = (i % (D / 8)) * 8;
     const bool kin = c.key0 + key < c.key_end;
@@ -207,7 +216,7 @@ attend_mfma_kernel(AttnArgs a) {
   stage_q();
   int64_t noff = q_off(nr, nhd, nsl);
 
-  for (int32_t g0 = wave * 32; g0 < c.n; g0 += 4 * 32) {
+  for (int32_t g0 = wave * 32; g0 < c.n; g0 += NWV * 32) {
     const bool live = csl >= 0;
     const int32_t row = cr;
     const int32_t head = chd;
@@ -216,11 +225,11 @@ attend_mfma_kernel(AttnArgs a) {
     V8 bq[D / 16];
 #pragma unroll
     for (int k = 0; k < D / 16; ++k) bq[k] = ld16<V8>(&rw[col * KS + 16 * k + 8 * h]);
-    if (g0 + 4 * 32 < c.n) fetch(noff);
+    if (g0 + NWV * 32 < c.n) fetch(noff);
     cr = nr;
     chd = nhd;
     csl = nsl;
-    load_idx(g0 + 8 * 32, nr, nhd, nsl);
+    load_idx(g0 + 2 * NWV * 32, nr, nhd, nsl);
 
     // S^T tiles: the KT chains interleave (independent MFMAs back to back),
     // each K-step's operands read together.
@@ -311,7 +320,7 @@ attend_mfma_kernel(AttnArgs a) {
     if constexpr (kOnesSum) l = lt[0];
 
     const int64_t dst = live ? part_row(a, c, row, head) * a.slots + slot : -1;
-    const bool more = g0 + 4 * 32 < c.n;
+    const bool more = g0 + NWV * 32 < c.n;
     // o[dt][v] is feature 32dt + 8(v/4) + 4h + v%4 of this lane's query.
     // Stores go out after the next group's rows are staged, so the wait for
     // those rows never includes them.
@@ -368,7 +377,7 @@ attend_mfma_kernel(AttnArgs a) {
 template <typename T, typename A, int D, int BS>
 static int launch_attend(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
   dim3 grid(static_cast<unsigned>(a.seg ? a.seg_cap : a.n_blocks), static_cast<unsigned>(n_cols));
-  hipLaunchKernelGGL((attend_mfma_kernel<T, A, D, BS>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((attend_mfma_kernel<T, A, D, BS>), grid, dim3(64 * attend_waves(D, BS)), 0, st, a);
   return check_launch("moba_attend (mfma)");
 }
 
@@ -416,16 +425,24 @@ int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hip
 // inside the workgroup, so the partial buffer is [.., slots, D], not
 // slots x sub-tiles. Semantics: src/moba/kernels/moba_bwd.py:216-394.
 // ---------------------------------------------------------------------------
-template <typename T, typename A, int D, int BS, int NQ>
-__global__ void __launch_bounds__(BS * 2, (D == 64 && BS == 128) ? 2 : 1)
+template <typename T, typename A, int D, int BS, int NQ, int ST>
+__global__ void __launch_bounds__(BS * 2 * ST, (D == 64 && BS == 128) ? 2 : 1)
 bwd_mfma_kernel(AttnArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::vec;
   using Sc = typename M::scalar;
   // NQ: queries per step (64; 32 at head_dim 128 with blocks under 128 keys)
   constexpr int QT = NQ / 32;   // query tiles of 32
-  constexpr int NW = BS / 32;   // waves: 32 keys each
-  constexpr int NT = NW * 64;   // threads
+  constexpr int NW = BS / 32;   // waves per stream: 32 keys each
+  constexpr int NT = NW * 64;   // threads per stream
+  constexpr int NTA = NT * ST;  // threads
+  // ST = 2: two streams of waves walk alternate steps of the column against
+  // the same keys, each with its own rows, dS^T and dK / dV sums (added at
+  // the end). K and V then sit row-major in LDS instead of in each lane's
+  // registers (S / dP read their B operands from there, dQ its K^T operand
+  // by transposing reads), which keeps a wave within 256 registers so a CU
+  // runs two of them per SIMD.
+  constexpr bool kKV = ST > 1;
   constexpr int DT = D / 32;
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
   constexpr int KTS = BS + 8;   // row stride of K^T ([d][key])
@@ -433,14 +450,17 @@ bwd_mfma_kernel(AttnArgs a) {
   // 8-byte dS writes land on distinct bank pairs (NQ + 8 paired keys c and
   // c + 16; measured 2% faster at 512K).
   constexpr int QS2 = NQ + 4;
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * KTS];
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[NQ * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Os[NQ * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t DSt[BS * QS2];
-  __shared__ __attribute__((aligned(16))) float s_lse[NQ];
-  __shared__ __attribute__((aligned(16))) float s_delta[NQ];
-  __shared__ __attribute__((aligned(16))) int s_lim[NQ];
-  __shared__ int64_t s_dst[NQ];
+  // K^T ([d][key]) for one stream, or K and V ([key][d]) for two.
+  __shared__ __attribute__((aligned(16))) uint16_t Kl[kKV ? 2 * BS * RS : D * KTS];
+  // Per stream: Q rows, dO rows, dS^T. One array, so that the float32
+  // hand-over of dK / dV between the streams can reuse all of it.
+  constexpr int kRows = 2 * NQ * RS + BS * QS2;
+  __shared__ __attribute__((aligned(16))) uint16_t Sm[ST * kRows];
+  __shared__ __attribute__((aligned(16))) float s_lse_[ST][NQ];
+  __shared__ __attribute__((aligned(16))) float s_delta_[ST][NQ];
+  __shared__ __attribute__((aligned(16))) int s_lim_[ST][NQ];
+  __shared__ int64_t s_dst_[ST][NQ];
+  static_assert((NQ * RS * 2) % 16 == 0 && (kRows * 2) % 16 == 0, "16-byte aligned carving");
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
   if (c.skip) return;  // past the segment list (uniform)
@@ -455,7 +475,19 @@ bwd_mfma_kernel(AttnArgs a) {
   if (key_lim <= 0) return;  // uniform
 
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int stream = kKV ? tid / NT : 0;
+  const int stid = kKV ? tid % NT : tid;  // thread index within the stream
+  const int wave = stid >> 6;
+  uint16_t* Qs = Sm + stream * kRows;
+  uint16_t* Os = Qs + NQ * RS;
+  uint16_t* DSt = Os + NQ * RS;
+  uint16_t* Kt = Kl;          // one stream
+  uint16_t* Ks = Kl;          // two streams
+  uint16_t* Vs = Kl + BS * RS;
+  float* s_lse = s_lse_[stream];
+  float* s_delta = s_delta_[stream];
+  int* s_lim = s_lim_[stream];
+  int64_t* s_dst = s_dst_[stream];
   const int h = lane >> 5;
   const int col = lane & 31;
   const int mykey = wave * 32 + col;  // the key this lane holds in S / dP / dV / dK
@@ -471,7 +503,7 @@ bwd_mfma_kernel(AttnArgs a) {
   // flight; everything is waited for once, before the step's stores.
   constexpr int CH = NQ * D / 8 / NT;  // 16-byte chunks per thread per tensor
   static_assert(NQ * D / 8 % NT == 0, "row chunks must tile the workgroup");
-  const int qi = tid % NQ;
+  const int qi = stid % NQ;
   const int32_t last = c.n > 0 ? c.n - 1 : 0;
   int32_t i_row = 0, i_head = 0, i_slot = -1;   // raw entry, step g + 2
   auto load_idx = [&](int32_t g) {
@@ -483,7 +515,8 @@ bwd_mfma_kernel(AttnArgs a) {
   };
   int64_t n_pr = 0, n_dst = -1;                 // derived, step g + 1
   int n_lim = -1;
-  __shared__ int64_t s_qoff[NQ];
+  __shared__ int64_t s_qoff_[ST][NQ];
+  int64_t* s_qoff = s_qoff_[stream];
   auto derive = [&]() {
     const bool ok = i_slot >= 0;
     const int64_t pr = part_row(a, c, i_row, i_head);
@@ -492,7 +525,7 @@ bwd_mfma_kernel(AttnArgs a) {
     n_pr = ok ? pr : 0;
     n_dst = ok ? pr * a.slots + i_slot : -1;
     n_lim = ok ? min(key_lim - 1, row_lim) : -1;
-    if (tid < NQ) s_qoff[tid] = ok ? q_offset(a, c, i_row, i_head) : -1;
+    if (stid < NQ) s_qoff[stid] = ok ? q_offset(a, c, i_row, i_head) : -1;
   };
   u32x4 pq[CH], po[CH];
   bool pv[CH];  // chunk belongs to a live entry (zeroed when staged)
@@ -503,7 +536,7 @@ bwd_mfma_kernel(AttnArgs a) {
     n_dl = ld.y;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      const int i = tid + u * NT;
+      const int i = stid + u * NT;
       const int64_t o = s_qoff[i / (D / 8)];
       const int64_t off = (o >= 0 ? o : 0) + (i % (D / 8)) * 8;
       pq[u] = *reinterpret_cast<const u32x4*>(Qg + off);
@@ -520,20 +553,21 @@ bwd_mfma_kernel(AttnArgs a) {
   // its entries are in; then K^T is written. Loads are unconditional: keys
   // past the block's end read a valid row (K^T zeroes them; their S and dP
   // are masked and their dK / dV never stored).
-  constexpr int KTN = BS * D / 8 / NT;  // 16-byte K chunks per thread for K^T
-  static_assert(BS * D / 8 % NT == 0, "K chunks must tile the workgroup");
-  if (c.n > 0) load_idx(0);
-  u32x4 ktc[KTN];
+  constexpr int KTN = BS * D / 8 / NTA;  // 16-byte K (and V) chunks per thread
+  static_assert(BS * D / 8 % NTA == 0, "K chunks must tile the workgroup");
+  if (c.n > 0) load_idx(stream * NQ);
+  u32x4 ktc[KTN], vtc[kKV ? KTN : 1];
 #pragma unroll
   for (int u = 0; u < KTN; ++u) {
-    const int i = tid + u * NT;
+    const int i = tid + u * NTA;
     const int key = i / (D / 8);
     const int d8 = (i % (D / 8)) * 8;
-    ktc[u] = *reinterpret_cast<const u32x4*>(
-        Kg + ((c.tok0 + (key < key_lim ? key : 0)) * a.h_kv + c.hk) * D + d8);
+    const int64_t off = ((c.tok0 + (key < key_lim ? key : 0)) * a.h_kv + c.hk) * D + d8;
+    ktc[u] = *reinterpret_cast<const u32x4*>(Kg + off);
+    if constexpr (kKV) vtc[u] = *reinterpret_cast<const u32x4*>(Vg + off);
   }
-  V8 kb[D / 16], vb[D / 16];
-  {
+  V8 kb[kKV ? 1 : D / 16], vb[kKV ? 1 : D / 16];
+  if constexpr (!kKV) {
     const int64_t off = ((c.tok0 + (mykey < key_lim ? mykey : 0)) * a.h_kv + c.hk) * D + 8 * h;
 #pragma unroll
     for (int k = 0; k < D / 16; ++k) {
@@ -545,17 +579,22 @@ bwd_mfma_kernel(AttnArgs a) {
     derive();
     __syncthreads();
     fetch();
-    load_idx(NQ);
+    load_idx(stream * NQ + ST * NQ);
   }
 #pragma unroll
   for (int u = 0; u < KTN; ++u) {
-    const int i = tid + u * NT;
+    const int i = tid + u * NTA;
     const int key = i / (D / 8);
     const int d8 = (i % (D / 8)) * 8;
     const u32x4 kv = key < key_lim ? ktc[u] : u32x4{0, 0, 0, 0};
-    const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kv);
+    if constexpr (kKV) {
+      *reinterpret_cast<u32x4*>(&Ks[key * RS + d8]) = kv;
+      *reinterpret_cast<u32x4*>(&Vs[key * RS + d8]) = key < key_lim ? vtc[u] : u32x4{0, 0, 0, 0};
+    } else {
+      const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kv);
 #pragma unroll
-    for (int w = 0; w < 8; ++w) Kt[(d8 + w) * KTS + key] = ke[w];
+      for (int w = 0; w < 8; ++w) Kt[(d8 + w) * KTS + key] = ke[w];
+    }
   }
   if (c.n > 0) {
     c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
@@ -565,22 +604,27 @@ bwd_mfma_kernel(AttnArgs a) {
   // the loop's wait counts start from an empty queue on every path.
   __builtin_amdgcn_s_waitcnt(0x0f70);
 
-  for (int32_t g0 = 0; g0 < c.n; g0 += NQ) {
+  // Every stream runs the same number of iterations (the barriers are
+  // shared); a stream past the column's end runs a dead step: zero rows,
+  // every entry hidden, nothing stored.
+  for (int32_t base = 0; base < c.n; base += ST * NQ) {
+    const int32_t g0 = base + stream * NQ;
+    const bool act = g0 < c.n;
     __syncthreads();  // previous step fully consumed; s_qoff of step g + 1 visible
-    if (tid < NQ) {
-      s_lim[tid] = c_lim;
-      s_lse[tid] = c_lse;
-      s_delta[tid] = c_dl;
-      s_dst[tid] = c_dst;
+    if (stid < NQ) {
+      s_lim[stid] = act ? c_lim : -1;
+      s_lse[stid] = c_lse;
+      s_delta[stid] = c_dl;
+      s_dst[stid] = act ? c_dst : -1;
     }
     // Q and dO rows, row-major; the dV / dK products read them transposed.
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      const int i = tid + u * NT;
+      const int i = stid + u * NT;
       const int q = i / (D / 8);
       const int d8 = (i % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = pv[u] ? pq[u] : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = pv[u] ? po[u] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = pv[u] && act ? pq[u] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = pv[u] && act ? po[u] : u32x4{0, 0, 0, 0};
     }
     __syncthreads();
     // Every entry of the step sees the whole block (a strictly past, full
@@ -590,10 +634,10 @@ bwd_mfma_kernel(AttnArgs a) {
     // uniform over the workgroup.
     const bool all_visible = __all(lane >= NQ || s_lim[lane < NQ ? lane : 0] == BS - 1 ||
                                    s_lim[lane < NQ ? lane : 0] < 0);
-    const bool more = g0 + NQ < c.n;
+    const bool more = g0 + ST * NQ < c.n;
     if (more) {
       fetch();
-      load_idx(g0 + 2 * NQ);
+      load_idx(g0 + 2 * ST * NQ);
     }
 
     // S and dP for this wave's 32 keys and each 32-query tile; lane <->
@@ -605,8 +649,13 @@ bwd_mfma_kernel(AttnArgs a) {
       const uint16_t* oa = &Os[(qt * 32 + col) * RS + 8 * h];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
-        sacc = M::mma(ld16<V8>(qa + 16 * k), kb[k], sacc);
-        pacc = M::mma(ld16<V8>(oa + 16 * k), vb[k], pacc);
+        if constexpr (kKV) {
+          sacc = M::mma(ld16<V8>(qa + 16 * k), ld16<V8>(&Ks[mykey * RS + 16 * k + 8 * h]), sacc);
+          pacc = M::mma(ld16<V8>(oa + 16 * k), ld16<V8>(&Vs[mykey * RS + 16 * k + 8 * h]), pacc);
+        } else {
+          sacc = M::mma(ld16<V8>(qa + 16 * k), kb[k], sacc);
+          pacc = M::mma(ld16<V8>(oa + 16 * k), vb[k], pacc);
+        }
       }
       V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
       auto softmax = [&](auto masked) {
@@ -678,11 +727,24 @@ bwd_mfma_kernel(AttnArgs a) {
       const int dt = tt % DT, qt = tt / DT;
       dq[t] = floatx16_t{};
 #pragma unroll
-      for (int j = 0; j < BS / 16; ++j)
-        dq[t] = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
-                       ld_tr2<V8>(&DSt[(16 * j + tr_key) * QS2 + qt * 32 + tr_q],
-                                  &DSt[(16 * j + 4 + tr_key) * QS2 + qt * 32 + tr_q]),
-                       dq[t]);
+      for (int j = 0; j < BS / 16; ++j) {
+        if constexpr (kKV) {
+          // Both operands by transposing reads with the dV / dK pattern:
+          // lane (col, h) holds, at K slots 8h + 4m + [0, 4), the keys
+          // 16j + 8m + 4h + [0, 4) -- of feature 32dt + col of K (A) and of
+          // query 32qt + col of dS (B).
+          const int kr = 16 * j + 4 * h + ((lane & 15) >> 2);
+          const int c4 = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+          dq[t] = M::mma(ld_tr2<V8>(&Ks[kr * RS + dt * 32 + c4], &Ks[(kr + 8) * RS + dt * 32 + c4]),
+                         ld_tr2<V8>(&DSt[kr * QS2 + qt * 32 + c4], &DSt[(kr + 8) * QS2 + qt * 32 + c4]),
+                         dq[t]);
+        } else {
+          dq[t] = M::mma(ld16<V8>(&Kt[(dt * 32 + col) * KTS + 16 * j + 8 * h]),
+                         ld_tr2<V8>(&DSt[(16 * j + tr_key) * QS2 + qt * 32 + tr_q],
+                                    &DSt[(16 * j + 4 + tr_key) * QS2 + qt * 32 + tr_q]),
+                         dq[t]);
+        }
+      }
     }
     // dq[t][v] is feature 32dt + 8(v/4) + 4h + v%4 of query 32qt + col.
     if constexpr (sizeof(A) == 2) {
@@ -704,7 +766,7 @@ bwd_mfma_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
-        const int i = tid + u * NT;
+        const int i = stid + u * NT;
         const int q = i / (D / 8);
         const int d8 = (i % (D / 8)) * 8;
         const int64_t dst = s_dst[q];
@@ -732,6 +794,40 @@ bwd_mfma_kernel(AttnArgs a) {
     }
   }
 
+  if constexpr (kKV) {
+    // Stream 1 hands its float32 sums to stream 0 through the K / V LDS
+    // (free once every step is done), dK then dV; slot (dt, q4, wave, lane)
+    // holds four consecutive floats.
+    float4* xb = reinterpret_cast<float4*>(Kl);
+    static_assert(DT * 4 * NW * 64 * 16 <= sizeof(Kl), "dK / dV hand-over fits the K / V LDS");
+    auto hand_over = [&](floatx16_t (&acc)[DT]) {
+      __syncthreads();  // the previous use of this LDS is complete
+      if (stream == 1) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            xb[((dt * 4 + q4) * NW + wave) * 64 + lane] =
+                make_float4(acc[dt][4 * q4], acc[dt][4 * q4 + 1], acc[dt][4 * q4 + 2], acc[dt][4 * q4 + 3]);
+      }
+      __syncthreads();
+      if (stream == 0) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 o = xb[((dt * 4 + q4) * NW + wave) * 64 + lane];
+            acc[dt][4 * q4] += o.x;
+            acc[dt][4 * q4 + 1] += o.y;
+            acc[dt][4 * q4 + 2] += o.z;
+            acc[dt][4 * q4 + 3] += o.w;
+          }
+      }
+    };
+    hand_over(dk);
+    hand_over(dv);
+    if (stream != 0) return;
+  }
   // dK, dV of this lane's key: register v is feature 32dt + 8(v/4) + 4h + v%4.
   // A segment of a cut column leaves its float32 sums in its scratch slot
   // ([2][BS][D]: dK scaled, dV); the finishing pass adds the column's
@@ -773,12 +869,13 @@ bwd_mfma_kernel(AttnArgs a) {
 
 template <typename T, typename A, int D, int BS>
 static int launch_bwd(const AttnArgs& a, int64_t n_cols, hipStream_t st) {
-  // 64 queries per step; at head_dim 128 only with 128-key blocks (88 KiB of
-  // LDS, one workgroup per CU as the registers already require), since the
-  // smaller blocks' variants would spill.
-  constexpr int NQ = (D == 128 && BS != 128) ? 32 : 64;
+  // 64 queries per step at head_dim 64, 32 at 128 (wider steps spill). At
+  // head_dim 128 with 128-key blocks, two streams of 4 waves share the keys
+  // (K / V in LDS): 8 waves, 2 per SIMD, in 125 KiB of LDS.
+  constexpr int ST = (D == 128 && BS == 128) ? 2 : 1;
+  constexpr int NQ = D == 128 ? 32 : 64;
   dim3 grid(static_cast<unsigned>(a.seg ? a.seg_cap : a.n_blocks), static_cast<unsigned>(n_cols));
-  hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS, NQ>), grid, dim3(BS * 2), 0, st, a);
+  hipLaunchKernelGGL((bwd_mfma_kernel<T, A, D, BS, NQ, ST>), grid, dim3(BS * 2 * ST), 0, st, a);
   return check_launch("moba_bwd (mfma)");
 }
 
