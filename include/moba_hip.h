@@ -47,12 +47,13 @@ enum moba_status {
 
 enum moba_dtype { MOBA_BF16 = 0, MOBA_FP16 = 1, MOBA_FP32 = 2 };
 
-/* Library identity. moba_abi_version() is 5: (m, l) and (lse, delta) travel
+/* Library identity. moba_abi_version() is 6: (m, l) and (lse, delta) travel
  * as 8-byte pairs, the CSC index arrays take an element stride, the CSC
- * build can emit a segment list that attend and backward take, and its
- * workspace is sized by rows per sequence (version 1 took separate
- * statistics arrays; 2 had no index stride; 3 no segments; 4 sized the CSC
- * workspace by seq_len and ordered column entries by atomic cursors). */
+ * build can emit a segment list that attend and backward take, its
+ * workspace is sized by rows per sequence, and moba_bwd takes the dK / dV
+ * dtype (version 1 took separate statistics arrays; 2 had no index stride;
+ * 3 no segments; 4 sized the CSC workspace by seq_len and ordered column
+ * entries by atomic cursors; 5 wrote dK / dV in the input dtype only). */
 int moba_abi_version(void);
 const char* moba_last_error(void);
 const char* moba_status_string(int status);
@@ -237,8 +238,11 @@ int moba_bwd_delta(const void* out, const void* dout, const float* lse,
                    int64_t head_dim, int dtype, void* stream);
 
 /*
- * KV-block-major backward: dK, dV [B, S, Hkv, D] (input dtype, every key
- * written, zero for unselected blocks) and one dQ partial per (query, slot):
+ * KV-block-major backward: dK, dV [B, S, Hkv, D] (dkv_dtype: the input
+ * dtype, or MOBA_FP32 for the unrounded float32 sums, which a caller that
+ * adds the dK / dV of several calls -- query-head subsets of one kv head --
+ * rounds once at the end; every key written, zero for unselected blocks)
+ * and one dQ partial per (query, slot):
  * dq_part [B, Hq, S, slots, D] (acc_dtype). Replaces the kernel launch in
  * moba_backward (src/moba/kernels/moba_bwd.py:506-579; kernel
  * moba_bwd.py:216-394). lse_delta: the (lse, delta) pairs moba_bwd_delta
@@ -259,7 +263,7 @@ int moba_bwd(const void* q, const void* k, const void* v, const void* dout,
              int64_t index_cap, int64_t index_stride, const int32_t* segments,
              const int32_t* seg_split, const int32_t* seg_counts, int64_t seg_cap,
              float* seg_scratch, int64_t scratch_cap, int causal, int dtype,
-             int acc_dtype, void* stream);
+             int acc_dtype, int dkv_dtype, void* stream);
 
 /*
  * dQ [B, S, Hq, D] = sum over written slots of dq_part, gated by the

@@ -24,6 +24,7 @@ struct AttnArgs {
   void* part_acc;         // forward: acc partials; backward: dq partials
   void* dk;               // backward only
   void* dv;               // backward only
+  int dkv_f32;            // backward: dK / dV stored as float32, not the input dtype
   int64_t S;              // padded S, or packed token count T
   int64_t h_q, h_kv, D, n_blocks, bs, slots, cap;
   int causal;

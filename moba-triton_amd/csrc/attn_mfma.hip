@@ -853,17 +853,22 @@ bwd_mfma_kernel(AttnArgs a) {
   }
   if (mykey < key_lim) {
     const int64_t off = ((c.tok0 + mykey) * a.h_kv + c.hk) * D + 4 * h;
-    T* dK = static_cast<T*>(a.dk) + off;
-    T* dV = static_cast<T*>(a.dv) + off;
+    auto store_kv = [&](auto* dK, auto* dV) {
+      using E = std::remove_pointer_t<decltype(dK)>;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        store4<T>(dK + dt * 32 + 8 * q4, dk[dt][4 * q4] * a.scale, dk[dt][4 * q4 + 1] * a.scale,
-                  dk[dt][4 * q4 + 2] * a.scale, dk[dt][4 * q4 + 3] * a.scale);
-        store4<T>(dV + dt * 32 + 8 * q4, dv[dt][4 * q4], dv[dt][4 * q4 + 1],
-                  dv[dt][4 * q4 + 2], dv[dt][4 * q4 + 3]);
-      }
+        for (int q4 = 0; q4 < 4; ++q4) {
+          store4<E>(dK + dt * 32 + 8 * q4, dk[dt][4 * q4] * a.scale, dk[dt][4 * q4 + 1] * a.scale,
+                    dk[dt][4 * q4 + 2] * a.scale, dk[dt][4 * q4 + 3] * a.scale);
+          store4<E>(dV + dt * 32 + 8 * q4, dv[dt][4 * q4], dv[dt][4 * q4 + 1],
+                    dv[dt][4 * q4 + 2], dv[dt][4 * q4 + 3]);
+        }
+    };
+    if (a.dkv_f32)  // uniform: float32 sums for a caller that adds several calls
+      store_kv(static_cast<float*>(a.dk) + off, static_cast<float*>(a.dv) + off);
+    else
+      store_kv(static_cast<T*>(a.dk) + off, static_cast<T*>(a.dv) + off);
   }
 }
 

@@ -215,15 +215,20 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
       dv[u] = adv;
     }
   }
-  T* dK = static_cast<T*>(a.dk);
-  T* dV = static_cast<T*>(a.dv);
   for (int u = 0; u < own; ++u) {
     const int64_t i = threadIdx.x + static_cast<int64_t>(u) * blockDim.x;
     const int64_t j = i / D, d = i % D;
     if (kt0 + j >= a.bs || c.key0 + kt0 + j >= c.key_end) continue;
     const int64_t off = ((c.tok0 + kt0 + j) * a.h_kv + c.hk) * D + d;
-    Elem<T>::store(dK, off, static_cast<float>(dk[u] * static_cast<Acc>(a.scale)));
-    Elem<T>::store(dV, off, static_cast<float>(dv[u]));
+    const float gk = static_cast<float>(dk[u] * static_cast<Acc>(a.scale));
+    const float gv = static_cast<float>(dv[u]);
+    if (a.dkv_f32) {
+      static_cast<float*>(a.dk)[off] = gk;
+      static_cast<float*>(a.dv)[off] = gv;
+    } else {
+      Elem<T>::store(static_cast<T*>(a.dk), off, gk);
+      Elem<T>::store(static_cast<T*>(a.dv), off, gv);
+    }
   }
 }
 
@@ -544,6 +549,11 @@ seg_finish_kernel(AttnArgs a) {
       sv.x += y.x; sv.y += y.y; sv.z += y.z; sv.w += y.w;
     }
     const int64_t off = ((c.tok0 + key) * a.h_kv + c.hk) * a.D + 4 * c4;
+    if (a.dkv_f32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(a.dk) + off) = sk;
+      *reinterpret_cast<float4*>(static_cast<float*>(a.dv) + off) = sv;
+      continue;
+    }
     Elem<T>::store(dK, off, sk.x); Elem<T>::store(dK, off + 1, sk.y);
     Elem<T>::store(dK, off + 2, sk.z); Elem<T>::store(dK, off + 3, sk.w);
     Elem<T>::store(dV, off, sv.x); Elem<T>::store(dV, off + 1, sv.y);
@@ -762,7 +772,7 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
                         int64_t index_cap, int64_t index_stride, const int32_t* segments,
                         const int32_t* seg_split, const int32_t* seg_counts, int64_t seg_cap,
                         float* seg_scratch, int64_t scratch_cap, int causal, int dtype,
-                        int acc_dtype, void* stream) {
+                        int acc_dtype, int dkv_dtype, void* stream) {
   using namespace moba;
   AttnArgs a;
   Geometry g;
@@ -774,6 +784,9 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
   if (!dout || !lse_delta || !dk || !dv || !dq_part)
     return fail(MOBA_ERR_INVALID, "null pointer");
   a.dout = dout; a.lse_delta = lse_delta; a.dk = dk; a.dv = dv; a.part_acc = dq_part;
+  if (dkv_dtype != dtype && dkv_dtype != MOBA_FP32)
+    return fail(MOBA_ERR_INVALID, "dkv_dtype must be the input dtype or float32");
+  a.dkv_f32 = dkv_dtype == MOBA_FP32 && dtype != MOBA_FP32;
   st = set_segments(&a, segments, seg_split, seg_counts, seg_cap);
   if (st) return st;
   if (a.seg) {

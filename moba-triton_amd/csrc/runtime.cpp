@@ -56,7 +56,7 @@ int make_geometry(Geometry* g, int64_t batch, int64_t seq_len,
 
 extern "C" {
 
-int moba_abi_version(void) { return 5; }
+int moba_abi_version(void) { return 6; }
 
 const char* moba_last_error(void) { return moba::g_last_error.c_str(); }
 

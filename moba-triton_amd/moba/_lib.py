@@ -48,7 +48,7 @@ SIGNATURES = {
     "moba_bwd_delta": (_I, [_P, _P, _P, _P, _L, _L, _L, _L, _I, _P]),
     "moba_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                       _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L, _P, _L,
-                      _I, _I, _I, _P]),
+                      _I, _I, _I, _I, _P]),
     "moba_dq_reduce": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _L, _I, _I, _P]),
 }
 
@@ -60,7 +60,7 @@ class LibraryMissing(RuntimeError):
 
 
 # Version of include/moba_hip.h these bindings follow.
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def load() -> ctypes.CDLL:

@@ -91,7 +91,8 @@ class MoBAAttentionFunction(torch.autograd.Function):
             dq, dk, dv = moba_backward(dout, q, k, v, out, lse, part_m, ctx.cfg, idx,
                                        causal=ctx.causal)
             return dq, dk, dv, None, None, None, None, None
-        # Chunks holding part of a kv head's group add into float32 dK / dV.
+        # Chunks holding part of a kv head's group add their unrounded
+        # float32 dK / dV; the sum is rounded once.
         split = any((c[4], c[5]) != (0, group) for c in chunks)
         dq = torch.empty_like(q)
         dk, dv = ((torch.zeros(k.shape, dtype=torch.float32, device=k.device),
@@ -103,11 +104,11 @@ class MoBAAttentionFunction(torch.autograd.Function):
             g = moba_backward(_piece(dout, b0, b1, hq0, hq1), _piece(q, b0, b1, hq0, hq1),
                               _piece(k, b0, b1, hk0, hk1), _piece(v, b0, b1, hk0, hk1),
                               _piece(out, b0, b1, hq0, hq1), lse, part_m, ctx.cfg, idx,
-                              causal=ctx.causal)
+                              causal=ctx.causal, dkv_dtype=torch.float32 if split else None)
             dq[b0:b1, :, hq0:hq1] = g[0]
             if split:
-                dk[b0:b1, :, hk0:hk1] += g[1].float()
-                dv[b0:b1, :, hk0:hk1] += g[2].float()
+                dk[b0:b1, :, hk0:hk1] += g[1]
+                dv[b0:b1, :, hk0:hk1] += g[2]
             else:
                 dk[b0:b1, :, hk0:hk1] = g[1]
                 dv[b0:b1, :, hk0:hk1] = g[2]

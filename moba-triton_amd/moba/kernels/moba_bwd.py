@@ -51,7 +51,10 @@ def bwd_kernel(dout, q, k, v, lse_delta, cfg: MoBAConfig, index: CSCIndex, dk, d
                causal: bool = True) -> None:
     """The KV-block-major backward launch (`moba_bwd.py:216-394`): dK, dV
     and one dQ partial per (query, slot), from contiguous q / k / v / dO on
-    the GPU and the (lse, delta) pairs of `compute_delta`."""
+    the GPU and the (lse, delta) pairs of `compute_delta`. dk / dv are in
+    q's dtype, or float32 for the unrounded sums."""
+    if dk.dtype != dv.dtype or dk.dtype not in (q.dtype, torch.float32):
+        raise ValueError(f"dk / dv must both be {q.dtype} or float32, got {dk.dtype}, {dv.dtype}")
     b, s, h_q, d = q.shape
     h_kv = k.shape[2]
     dev = q.device
@@ -73,12 +76,16 @@ def bwd_kernel(dout, q, k, v, lse_delta, cfg: MoBAConfig, index: CSCIndex, dk, d
               _lib.ptr(index.segments), _lib.ptr(index.seg_split), _lib.ptr(index.seg_counts),
               index.seg_cap, _lib.ptr(scratch), scratch_cap, int(bool(causal)),
               _lib.DTYPE_CODE[q.dtype], _lib.DTYPE_CODE[dq_part.dtype],
-              _lib.stream_handle(dev))
+              _lib.DTYPE_CODE[dk.dtype], _lib.stream_handle(dev))
 
 
 def moba_backward(dout, q, k, v, out, lse, part_m, cfg: MoBAConfig, index: CSCIndex,
-                  causal: bool = True):
+                  causal: bool = True, dkv_dtype: torch.dtype | None = None):
     """Gradients of the MoBA forward (`moba_bwd.py:506-579`).
+
+    dkv_dtype: None (q's dtype) or torch.float32, for dK / dV sums that the
+    caller adds to others (the query-head subsets of one kv head) and
+    rounds once.
 
     Returns:
         (dq, dk, dv) shaped like q, k, v; dk / dv carry H_kv heads, each
@@ -91,8 +98,8 @@ def moba_backward(dout, q, k, v, out, lse, part_m, cfg: MoBAConfig, index: CSCIn
     q, k, v = (_lib.aligned_contiguous(t) for t in (q, k, v))
     dout = _lib.aligned_contiguous(dout.to(q.dtype))
     lse_delta = compute_delta(out, dout, lse)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
+    dk = torch.empty_like(k, dtype=dkv_dtype)
+    dv = torch.empty_like(v, dtype=dkv_dtype)
     dq_part = torch.empty((b, h_q, s, index.max_slots, d), device=dev, dtype=q.dtype)
     bwd_kernel(dout, q, k, v, lse_delta, cfg, index, dk, dv, dq_part, causal=causal)
     return reduce_dq(dq_part, part_m, q.dtype), dk, dv

@@ -20,7 +20,7 @@ def declared_functions():
 
 def test_library_loads():
     lib = _lib.load()
-    assert lib.moba_abi_version() == 5
+    assert lib.moba_abi_version() == 6
 
 
 def test_every_declared_symbol_is_exported_and_bound():
