@@ -167,6 +167,35 @@ __device__ inline void insert_exact(float (&val)[M], int (&idx)[M], float s, int
   }
 }
 
+// val / idx <- the best M of its union with pv / pi (both sorted by (score
+// desc, id asc), ids disjoint), sorted: the better of val[p] and pv[M-1-p]
+// for every p are the best M of the union, in an order that falls then
+// rises (bitonic), which log2(M) half-cleaner stages sort. M is a power of
+// two.
+template <int M>
+__device__ inline void merge_top(float (&val)[M], int (&idx)[M], const float (&pv)[M],
+                                 const int (&pi)[M]) {
+  static_assert((M & (M - 1)) == 0, "bitonic merge needs a power of two");
+#pragma unroll
+  for (int p = 0; p < M; ++p)
+    if (ranks_before(pv[M - 1 - p], pi[M - 1 - p], val[p], idx[p])) {
+      val[p] = pv[M - 1 - p];
+      idx[p] = pi[M - 1 - p];
+    }
+#pragma unroll
+  for (int st = M / 2; st > 0; st >>= 1)
+#pragma unroll
+    for (int p = 0; p < M; ++p)
+      if ((p & st) == 0 && ranks_before(val[p + st], idx[p + st], val[p], idx[p])) {
+        const float tv = val[p];
+        const int ti = idx[p];
+        val[p] = val[p + st];
+        idx[p] = idx[p + st];
+        val[p + st] = tv;
+        idx[p + st] = ti;
+      }
+}
+
 // Branch-free insertion into a list sorted by value only (approximate scores;
 // ties among them are settled later by the exact rescoring).
 template <int M>
@@ -302,18 +331,28 @@ gate_exact_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 // Queue kernel: one wave per queued query. Lanes split the candidates, keep
 // exact top-T lists, and merge them with a butterfly over the wave.
 // ---------------------------------------------------------------------------
-template <typename T, int TMAX>
-__global__ void __launch_bounds__(256)
+// Lanes per queued query (8 waves: 256 registers each).
+template <typename T> constexpr int queue_threads() { return 512; }
+template <typename T, int TMAX, int D>
+__global__ void __launch_bounds__(queue_threads<T>())
 gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                   int32_t* __restrict__ out, const int32_t* __restrict__ cu,
                   int64_t S, int64_t rows_per_seq, int64_t h_q, int64_t h_kv,
-                  int D, int64_t n_blocks, int bs, int take, int cur, int slots,
+                  int64_t n_blocks, int bs, int take, int cur, int slots,
                   const int64_t* __restrict__ queue, const int* __restrict__ queue_len) {
-  // One workgroup per queued query: 256 lanes split its candidates, each
+  // One workgroup per queued query: its lanes split the candidates, each
   // keeps an exact top-T list, the lists merge with a butterfly inside each
-  // wave and then across the four waves through LDS.
-  __shared__ float s_v[4][TMAX];
-  __shared__ int s_i[4][TMAX];
+  // wave and then across the waves through LDS. A queued query is rare,
+  // so its time is the latency of one workgroup, set by the memory round
+  // trips of its candidate loop: the query row sits in registers and each
+  // lane requests the rows of U blocks before it scores any of them
+  // (float64 products and sum, as exact_score): at head_dim 64, 4096
+  // candidates take 2 round trips.
+  constexpr int U = 256 / D;  // rows in flight per lane
+  constexpr int C = D / 8;     // 16-byte chunks per row
+  constexpr int NWQ = queue_threads<T>() / 64;
+  __shared__ float s_v[NWQ][TMAX];
+  __shared__ int s_i[NWQ][TMAX];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t total = *queue_len;
@@ -332,38 +371,83 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     int idx[TMAX];
 #pragma unroll
     for (int p = 0; p < TMAX; ++p) { val[p] = -INFINITY; idx[p] = 0x7fffffff; }
-    for (int j = threadIdx.x; j < own; j += blockDim.x) {
-      const float s = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
-      if (ranks_before(s, j, val[take - 1], idx[take - 1])) insert_exact<TMAX>(val, idx, s, j);
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-      float pv[TMAX];
-      int pi[TMAX];
-#pragma unroll
-      for (int p = 0; p < TMAX; ++p) {
-        pv[p] = __shfl_xor(val[p], off);
-        pi[p] = __shfl_xor(idx[p], off);
+    if constexpr (Elem<T>::kCode == MOBA_FP16) {
+      // fp16's software conversion needs the registers: one candidate at a
+      // time per lane.
+      for (int j = threadIdx.x; j < own; j += blockDim.x) {
+        const float sc = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
+        if (ranks_before(sc, j, val[take - 1], idx[take - 1])) insert_exact<TMAX>(val, idx, sc, j);
       }
+    } else {
+      uint4 qv[C];
 #pragma unroll
-      for (int p = 0; p < TMAX; ++p)
-        if (pv[p] > -INFINITY) insert_exact<TMAX>(val, idx, pv[p], pi[p]);
+      for (int c = 0; c < C; ++c) qv[c] = *reinterpret_cast<const uint4*>(qrow + 8 * c);
+      for (int j0 = threadIdx.x; j0 < own; j0 += U * blockDim.x) {
+        uint4 kv[U][C];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = j0 + u * blockDim.x;
+          const T* krow = kb + static_cast<int64_t>(j < own ? j : 0) * D;
+#pragma unroll
+          for (int c = 0; c < C; ++c) kv[u][c] = *reinterpret_cast<const uint4*>(krow + 8 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = j0 + u * blockDim.x;
+          double acc = 0.0;
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            // Opaque to the compiler, so the row's float64 conversions stay
+            // in the loop (hoisted, they would take 2 * D registers).
+            uint4 qc = qv[c];
+            asm volatile("" : "+v"(qc.x), "+v"(qc.y), "+v"(qc.z), "+v"(qc.w));
+            const T* qe = reinterpret_cast<const T*>(&qc);
+            const T* ke = reinterpret_cast<const T*>(&kv[u][c]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              acc += static_cast<double>(Elem<T>::load(qe, i)) * static_cast<double>(Elem<T>::load(ke, i));
+          }
+          const float sc = Elem<T>::round(static_cast<float>(acc));
+          if (j < own && ranks_before(sc, j, val[take - 1], idx[take - 1]))
+            insert_exact<TMAX>(val, idx, sc, j);
+        }
+      }
     }
+    // Each wave's lists meet by a butterfly of merges, then the waves'
+    // lists by a butterfly over the first NWQ lanes of wave 0.
+    auto butterfly = [&](int from) {
+      for (int off = from; off > 0; off >>= 1) {
+        float pv[TMAX];
+        int pi[TMAX];
+#pragma unroll
+        for (int p = 0; p < TMAX; ++p) {
+          pv[p] = __shfl_xor(val[p], off);
+          pi[p] = __shfl_xor(idx[p], off);
+        }
+        merge_top<TMAX>(val, idx, pv, pi);
+      }
+    };
+    butterfly(32);
     if (lane == 0) {
 #pragma unroll
       for (int p = 0; p < TMAX; ++p) { s_v[wave][p] = val[p]; s_i[wave][p] = idx[p]; }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < 4; ++w)
+    if (wave == 0) {
+#pragma unroll
+      for (int p = 0; p < TMAX; ++p) {
+        val[p] = lane < NWQ ? s_v[lane][p] : -INFINITY;
+        idx[p] = lane < NWQ ? s_i[lane][p] : 0x7fffffff;
+      }
+      butterfly(NWQ / 2);
+      if (lane == 0) {
+        int n_sel = 0;
 #pragma unroll
         for (int p = 0; p < TMAX; ++p)
-          if (s_v[w][p] > -INFINITY) insert_exact<TMAX>(val, idx, s_v[w][p], s_i[w][p]);
-      int n_sel = 0;
-#pragma unroll
-      for (int p = 0; p < TMAX; ++p)
-        if (p < take && val[p] > -INFINITY) n_sel = p + 1;
-      emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
-                        out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
+          if (p < take && val[p] > -INFINITY) n_sel = p + 1;
+        emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
+                          out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
+      }
     }
     __syncthreads();
   }
@@ -954,18 +1038,16 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   if (rc) return rc;
   // Queries whose approximate evidence was insufficient: exact rescoring,
   // one wave per query.
-  if (take <= 8)
-    hipLaunchKernelGGL((gate_queue_kernel<T, 8>), dim3(2048), dim3(256), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
-                       g.seq_len, g.rows_per_seq, g.h_q, g.h_kv, static_cast<int>(g.head_dim),
-                       g.n_blocks, static_cast<int>(g.block_size), take, cur,
+  auto queue_launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(512), dim3(queue_threads<T>()), 0, st, static_cast<const T*>(q),
+                       static_cast<const T*>(kbar), out, cu, g.seq_len, g.rows_per_seq, g.h_q,
+                       g.h_kv, g.n_blocks, static_cast<int>(g.block_size), take, cur,
                        static_cast<int>(g.slots), ws.queue, ws.counter);
+  };
+  if (g.head_dim == 64)
+    take <= 8 ? queue_launch(gate_queue_kernel<T, 8, 64>) : queue_launch(gate_queue_kernel<T, 16, 64>);
   else
-    hipLaunchKernelGGL((gate_queue_kernel<T, 16>), dim3(2048), dim3(256), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
-                       g.seq_len, g.rows_per_seq, g.h_q, g.h_kv, static_cast<int>(g.head_dim),
-                       g.n_blocks, static_cast<int>(g.block_size), take, cur,
-                       static_cast<int>(g.slots), ws.queue, ws.counter);
+    take <= 8 ? queue_launch(gate_queue_kernel<T, 8, 128>) : queue_launch(gate_queue_kernel<T, 16, 128>);
   return check_launch("moba_gate (queue)");
   }
 }
