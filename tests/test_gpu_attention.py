@@ -449,3 +449,34 @@ def test_head_dim_256_forward_and_backward(device, dtype, bs):
                                ("dk", kk.grad, kc.grad, low[1]), ("dv", vv.grad, vc.grad, low[2])):
         assert_within_tolerance(ours, tr, max_abs_error(lo, tr), name)
         assert mean_abs_error(ours, tr) <= BF16_MEAN_ABS, name
+
+
+@pytest.mark.parametrize("shape,h_kv,segment", [((1, 1024, 4, 64), 4, "0"),      # MFMA, D 64
+                                                ((1, 1024, 8, 128), 2, "0"),     # two streams, D 128
+                                                ((1, 2048, 4, 64), 4, "64"),     # cut columns
+                                                ((1, 512, 2, 256), 2, "0")])     # FMA fallback
+def test_backward_float32_dkdv_rounds_to_the_default(device, monkeypatch, shape, h_kv, segment):
+    """moba_backward(dkv_dtype=float32) returns the float32 sums that the
+    default call rounds once: rounding them to bf16 gives its dK / dV bit for
+    bit, and dQ is unchanged."""
+    from moba.kernels.moba_bwd import moba_backward
+    from moba.kernels.moba_fwd import attend_partials
+    from moba.kernels.routing import ENV_SEGMENT
+
+    monkeypatch.setenv(ENV_SEGMENT, segment)
+    cfg = MoBAConfig(block_size=128, top_k=4)
+    q, k, v, do = (t.to(device) for t in make_qkv(shape, torch.bfloat16, seed=12, n=4))
+    k, v = k[:, :, :h_kv].contiguous(), v[:, :, :h_kv].contiguous()
+    index = build_csc_fused(q, k, cfg)
+    if segment != "0":
+        assert int(index.seg_counts[..., 1].sum()) > 0, "no column was cut"
+    part_m, part_l, part_acc = attend_partials(q, k, v, cfg, index)
+    out, lse = combine_partials(part_m, part_l, part_acc, q.dtype, return_lse=True)
+    dq, dk, dv = moba_backward(do, q, k, v, out, lse, part_m, cfg, index)
+    dq32, dk32, dv32 = moba_backward(do, q, k, v, out, lse, part_m, cfg, index,
+                                     dkv_dtype=torch.float32)
+    assert dk32.dtype is torch.float32 and dv32.dtype is torch.float32
+    assert torch.equal(dq, dq32)
+    assert torch.equal(dk, dk32.to(torch.bfloat16)) and torch.equal(dv, dv32.to(torch.bfloat16))
+    # Not already rounded: some sums carry bits below bf16's precision.
+    assert not torch.equal(dk32, dk32.to(torch.bfloat16).float())
