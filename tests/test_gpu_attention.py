@@ -480,3 +480,27 @@ def test_backward_float32_dkdv_rounds_to_the_default(device, monkeypatch, shape,
     assert torch.equal(dk, dk32.to(torch.bfloat16)) and torch.equal(dv, dv32.to(torch.bfloat16))
     # Not already rounded: some sums carry bits below bf16's precision.
     assert not torch.equal(dk32, dk32.to(torch.bfloat16).float())
+
+
+def test_packed_gqa_d128_backward_equals_each_sequence_alone(device):
+    """The two-stream head_dim-128 backward (128-key blocks) on packed GQA
+    input with ragged lengths: columns past a short sequence's end hold no
+    keys, and a stream may run a dead step. dQ per query is exact; dK / dV
+    sum a column in an order the packing changes, within the bf16 bars."""
+    cfg = MoBAConfig(block_size=128, top_k=4)
+    lens = [640, 128, 1000, 256]
+    cu = torch.tensor([0, 640, 768, 1768, 2024], dtype=torch.int32, device=device)
+    t = int(cu[-1])
+    q = make_qkv((1, t, 8, 128), torch.bfloat16, seed=15, device=device, n=1)[0]
+    k, v = make_qkv((1, t, 2, 128), torch.bfloat16, seed=16, device=device, n=2)
+    g = make_qkv((1, t, 8, 128), torch.bfloat16, seed=17, device=device, n=1)[0]
+    qq, kk, vv = (x.clone().requires_grad_(True) for x in (q, k, v))
+    moba_attention(qq, kk, vv, cfg, cu_seqlens=cu, max_seqlen=max(lens)).backward(g)
+    for r, ln in enumerate(lens):
+        lo = int(cu[r])
+        a = [x[:, lo:lo + ln].clone().requires_grad_(True) for x in (q, k, v)]
+        moba_attention(*a, cfg).backward(g[:, lo:lo + ln])
+        assert torch.equal(qq.grad[:, lo:lo + ln], a[0].grad), f"dq, sequence {r}"
+        for ours, alone in zip((kk.grad, vv.grad), a[1:]):
+            assert max_abs_error(ours[:, lo:lo + ln].float(), alone.grad.float()) <= BF16_MAX_ABS, f"sequence {r}"
+            assert mean_abs_error(ours[:, lo:lo + ln].float(), alone.grad.float()) <= BF16_MEAN_ABS, f"sequence {r}"
