@@ -21,6 +21,7 @@
 
 #include "common.h"
 
+
 namespace moba {
 
 __global__ void __launch_bounds__(256)
@@ -65,15 +66,27 @@ count_or_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __
   }
 }
 
-// Tiled count: kTileQ queries of one (row, query head) per workgroup,
-// kTileT threads each taking kTileQ / kTileT of them, counted in an LDS
-// histogram over the blocks the tile can see and written out as one row of
-// the unit count table (below). The LDS histogram keeps the global memory
-// traffic at one row per tile: the own block, which every query of a block
-// selects, would otherwise take 128 serialised global atomics.
+// Tiled count: tq queries of one (row, query head) per workgroup (a tile,
+// tq 256 or kTileQ), kTileT threads each taking up to
+// kTileQ / kTileT of them, counted in an LDS histogram over the blocks the
+// tile can see and written out as one row of the unit count table (below).
+// The LDS histogram keeps the global memory traffic at one row per tile:
+// the own block, which every query of a block selects, would otherwise take
+// 128 serialised global atomics.
 constexpr int kTileQ = 1024;
 typedef int32_t i32x3 __attribute__((ext_vector_type(3), aligned(4)));
 constexpr int kTileT = 256;
+
+// Queries per tile (a *unit* of the deterministic build is one tile of one
+// query head): 1024, or 256 when 1024-query tiles would give fewer than 512
+// units. The scatter walks a unit's entries in one serial chain, so a build
+// with few units waits on that chain (256 units at [1,64K,4,64]); with more
+// units, smaller tiles cost more in count-table traffic (units x columns)
+// than they save (measured: 64K 0.088 -> 0.072 ms, 128K no gain).
+inline int64_t tile_queries(int64_t batch, int64_t h_q, int64_t rows_per_seq) {
+  const int64_t units = batch * h_q * ((rows_per_seq + kTileQ - 1) / kTileQ);
+  return units < 512 ? 256 : kTileQ;
+}
 constexpr int kMaxBins = 16384;
 
 // Columns of the window [lo, lo + width) that queries seeing `nv` blocks can
@@ -104,7 +117,7 @@ __device__ inline void bin_add(int32_t* bins, int32_t blk, bool active) {
 // window [lo, lo + width), zeros where it sees none; grid (tiles, R * Hq).
 __global__ void __launch_bounds__(kTileT)
 tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restrict__ cu,
-                  int64_t S, int64_t h_q, int64_t n_blocks, int64_t bs, int slots,
+                  int64_t S, int64_t h_q, int64_t n_blocks, int64_t bs, int slots, int tq,
                   int32_t* __restrict__ table, int64_t lo, int64_t width) {
   extern __shared__ int32_t bins[];  // width counters (dynamic LDS)
   const int64_t rh = blockIdx.y;
@@ -112,14 +125,14 @@ tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restri
   const int64_t hq = rh % h_q;
   const bool packed = cu != nullptr;
   const SeqSpan sp = seq_span(cu, r, S);
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kTileQ;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tq;
   int32_t* trow = table + (rh * gridDim.x + blockIdx.x) * width;
   if (t0 >= sp.len) {
     for (int64_t b = threadIdx.x; b < width; b += kTileT) trow[b] = 0;
     return;
   }
-  const int64_t t_last = (t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len) - 1;
-  const int nvis = window_visible(t_last / bs + 1, n_blocks, lo, width);
+  const int64_t t_end = t0 + tq < sp.len ? t0 + tq : sp.len;  // this tile's queries: [t0, t_end)
+  const int nvis = window_visible((t_end - 1) / bs + 1, n_blocks, lo, width);
   for (int b = threadIdx.x; b < nvis; b += kTileT) bins[b] = 0;
   __syncthreads();
   // Query i of this thread: t0 + threadIdx.x + kTileT * i (a wave's lanes
@@ -133,9 +146,10 @@ tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restri
     for (int i = 0; i < QPT; ++i) {
       const int64_t t = t0 + threadIdx.x + kTileT * i;
       const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
-      const int4* p = reinterpret_cast<const int4*>(block_idx + (t < sp.len ? qid : 0) * 8);
-      ids[i][0] = t < sp.len ? p[0] : int4{-1, -1, -1, -1};
-      ids[i][1] = t < sp.len ? p[1] : int4{-1, -1, -1, -1};
+      const bool in = t < t_end;
+      const int4* p = reinterpret_cast<const int4*>(block_idx + (in ? qid : 0) * 8);
+      ids[i][0] = in ? p[0] : int4{-1, -1, -1, -1};
+      ids[i][1] = in ? p[1] : int4{-1, -1, -1, -1};
     }
 #pragma unroll
     for (int i = 0; i < QPT; ++i)
@@ -153,7 +167,7 @@ tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restri
       const int64_t t = t0 + threadIdx.x + kTileT * i;
       const int64_t qid = packed ? hq * S + sp.bos + t : (r * h_q + hq) * S + t;
       for (int j = 0; j < slots; ++j) {
-        const int32_t c = t < sp.len ? block_idx[qid * slots + j] - static_cast<int32_t>(lo) : -1;
+        const int32_t c = t < t_end ? block_idx[qid * slots + j] - static_cast<int32_t>(lo) : -1;
         bin_add(bins, c, c >= 0 && c < nvis);
       }
     }
@@ -169,7 +183,7 @@ tile_count_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restri
 // so the index -- and with it the order in which the backward sums a
 // column's dK / dV -- is the same on every build.
 //
-// A unit is one (row, query head, 1024-query tile); the units of one
+// A unit is one (row, query head, tile of tq queries); the units of one
 // (row, kv head) in (query head, tile) order are exactly the column order.
 // The count pass writes each unit's per-column counts to a table
 // [R, Hq, tiles, nb]; a two-level exclusive scan over the units turns it
@@ -260,7 +274,7 @@ det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restr
                    int slots, int64_t cap, const int32_t* __restrict__ table,
                    int32_t* __restrict__ row_indices, int32_t* __restrict__ head_indices,
                    int32_t* __restrict__ slot_of_pair, int64_t istride, bool records,
-                   int64_t lo, int64_t width) {
+                   int tq, int64_t lo, int64_t width) {
   extern __shared__ uint32_t cm[];  // (cursor, mask) per column of the window
   const int64_t tile = blockIdx.x;
   const int64_t rh = blockIdx.y;
@@ -270,9 +284,9 @@ det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restr
   const int64_t hk = hq / (h_q / h_kv);
   const bool packed = cu != nullptr;
   const SeqSpan sp = seq_span(cu, r, S);
-  const int64_t t0 = tile * kTileQ;
+  const int64_t t0 = tile * tq;
   if (t0 >= sp.len) return;
-  const int64_t t1 = t0 + kTileQ < sp.len ? t0 + kTileQ : sp.len;
+  const int64_t t1 = t0 + tq < sp.len ? t0 + tq : sp.len;
   const int nvis = window_visible((t1 - 1) / bs + 1, n_blocks, lo, width);
   if (nvis == 0) return;  // no column of the window is visible here
   const int32_t* trow = table + unit * width;
@@ -408,15 +422,16 @@ order_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ order,
   int rank = 0;
   for (int64_t base = 0; base < n_blocks; base += kTile) {
     const int64_t len = n_blocks - base < kTile ? n_blocks - base : kTile;
+    const int64_t len4 = (len + 3) & ~int64_t(3);  // whole 16-byte reads; only these are compared
     __syncthreads();
     // Past the end: -1 (no count is negative, so it is never larger), and
     // ids past every column (never a smaller id with an equal count).
-    for (int64_t i = threadIdx.x; i < kTile; i += blockDim.x) tile[i] = i < len ? cnt[base + i] : -1;
+    for (int64_t i = threadIdx.x; i < len4; i += blockDim.x) tile[i] = i < len ? cnt[base + i] : -1;
     __syncthreads();
     if (c < n_blocks) {
       const int4* t4 = reinterpret_cast<const int4*>(tile);
 #pragma unroll 4
-      for (int i4 = sub; i4 < kTile / 4; i4 += 8) {
+      for (int i4 = sub; i4 < len4 / 4; i4 += 8) {
         const int4 o = t4[i4];
         const int64_t id = base + 4 * i4;
         rank += (o.x > mine || (o.x == mine && id < c)) ? 1 : 0;
@@ -512,9 +527,9 @@ namespace {
 struct UnitPlan {
   int64_t tiles, units, chunk, nchunks;
 };
-UnitPlan unit_plan(int64_t rows_per_seq, int64_t h_q, int64_t h_kv) {
+UnitPlan unit_plan(int64_t rows_per_seq, int64_t h_q, int64_t h_kv, int64_t tq) {
   UnitPlan p;
-  p.tiles = moba::cdiv(rows_per_seq, moba::kTileQ);
+  p.tiles = moba::cdiv(rows_per_seq, tq);
   p.units = (h_kv > 0 ? h_q / h_kv : 1) * p.tiles;
   p.chunk = moba::cdiv(p.units, 64) > 16 ? moba::cdiv(p.units, 64) : 16;
   p.nchunks = moba::cdiv(p.units, p.chunk);
@@ -547,7 +562,7 @@ extern "C" size_t moba_csc_workspace_size(int64_t batch, int64_t rows_per_seq, i
   // Unit table and chunk sums of one column window. This is never smaller
   // than the atomic cursors of the untiled build (batch * h_kv * n_blocks),
   // which run in the same memory when the device lacks the LDS.
-  const UnitPlan p = unit_plan(rows_per_seq, h_q, h_kv);
+  const UnitPlan p = unit_plan(rows_per_seq, h_q, h_kv, moba::tile_queries(batch, h_q, rows_per_seq));
   const int64_t width = n_blocks < moba::kDetMaxCols ? n_blocks : moba::kDetMaxCols;
   const size_t det = sizeof(int32_t) * static_cast<size_t>(batch * width *
                                                           (h_q * p.tiles + h_kv * p.nchunks));
@@ -599,7 +614,8 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   const size_t det_lds = 8 * static_cast<size_t>(win);
   const bool tiled = det_lds_ok(det_lds);
   const int64_t bs_eff = cdiv(g.rows_per_seq, n_blocks);
-  const UnitPlan up = unit_plan(g.rows_per_seq, h_q, h_kv);
+  const int64_t tq = tile_queries(batch, h_q, g.rows_per_seq);
+  const UnitPlan up = unit_plan(g.rows_per_seq, h_q, h_kv, tq);
   const unsigned rhk = static_cast<unsigned>(batch * h_kv);
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq * slots, 256)),
             static_cast<unsigned>(batch * h_q));
@@ -612,8 +628,8 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
   auto window_counts = [&](int64_t lo, int64_t width, int32_t* nnz) {
     hipLaunchKernelGGL(tile_count_kernel, tgrid, dim3(kTileT),
                        static_cast<unsigned>(sizeof(int32_t) * width), s, block_idx, cu_seqlens,
-                       seq_len, h_q, n_blocks, bs_eff, static_cast<int>(slots), table, lo,
-                       width);
+                       seq_len, h_q, n_blocks, bs_eff, static_cast<int>(slots),
+                       static_cast<int>(tq), table, lo, width);
     hipLaunchKernelGGL(unit_chunk_kernel<0>,
                        dim3(static_cast<unsigned>(cdiv(width, 256)),
                             static_cast<unsigned>(up.nchunks), rhk),
@@ -631,7 +647,8 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
     hipLaunchKernelGGL(det_scatter_kernel, tgrid, dim3(64),
                        static_cast<unsigned>(8 * width), s, block_idx, cu_seqlens, seq_len, h_q,
                        h_kv, n_blocks, bs_eff, static_cast<int>(slots), cap, table, row_indices,
-                       head_indices, slot_of_pair, index_stride, records, lo, width);
+                       head_indices, slot_of_pair, index_stride, records, static_cast<int>(tq),
+                       lo, width);
   };
   if (tiled && n_win == 1) {
     window_counts(0, n_blocks, col_nnz);
