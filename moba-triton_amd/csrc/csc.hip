@@ -377,11 +377,36 @@ det_scatter_kernel(const int32_t* __restrict__ block_idx, const int32_t* __restr
   }
 }
 
+// Inclusive scan of x over a 1024-thread workgroup (every thread calls it):
+// a shuffle scan inside each wave, then each thread adds the totals of the
+// waves before its own. `total` receives the sum over the workgroup. wtot
+// is 16 ints of LDS, free again when the call returns.
+__device__ inline int32_t block_scan_1024(int32_t x, int32_t* wtot, int32_t& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wtot[wave] = x;
+  __syncthreads();
+  int32_t before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    const int32_t t = wtot[w];
+    before += w < wave ? t : 0;
+    sum += t;
+  }
+  __syncthreads();
+  total = sum;
+  return x + before;
+}
+
 // Exclusive scan of one (row, kv head)'s counts; one workgroup each.
 __global__ void __launch_bounds__(1024)
 scan_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ col_offsets,
             int64_t n_blocks) {
-  __shared__ int32_t buf[1024];
+  __shared__ int32_t wtot[16];
   const int64_t rh = blockIdx.x;
   const int32_t* cnt = col_nnz + rh * n_blocks;
   int32_t* off = col_offsets + rh * (n_blocks + 1);
@@ -389,17 +414,9 @@ scan_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ col_offse
   for (int64_t base = 0; base < n_blocks; base += 1024) {
     const int64_t i = base + threadIdx.x;
     const int32_t x = i < n_blocks ? cnt[i] : 0;
-    buf[threadIdx.x] = x;
-    __syncthreads();
-    for (int s = 1; s < 1024; s <<= 1) {
-      int32_t y = threadIdx.x >= s ? buf[threadIdx.x - s] : 0;
-      __syncthreads();
-      buf[threadIdx.x] += y;
-      __syncthreads();
-    }
-    if (i < n_blocks) off[i] = carry + buf[threadIdx.x] - x;
-    const int32_t total = buf[1023];
-    __syncthreads();
+    int32_t total;
+    const int32_t inc = block_scan_1024(x, wtot, total);
+    if (i < n_blocks) off[i] = carry + inc - x;
     carry += total;
   }
   if (threadIdx.x == 0) off[n_blocks] = carry;
@@ -460,21 +477,10 @@ __global__ void __launch_bounds__(1024)
 seg_build_kernel(const int32_t* __restrict__ col_nnz, const int32_t* __restrict__ order,
                  int64_t n_blocks, int64_t seg_len, int max_seg, int32_t* __restrict__ seg,
                  int32_t* __restrict__ split, int32_t* __restrict__ counts, int64_t cap) {
-  __shared__ int32_t sa[1024], sb[1024];
+  __shared__ int32_t wtot[16];
   const int64_t rh = blockIdx.x;
-  const int tid = threadIdx.x;
   const int64_t extra_cap = cap - n_blocks;
-  // Inclusive scan of sa (and sb) over the workgroup.
-  auto scan = [&](bool both) {
-    for (int w = 1; w < 1024; w <<= 1) {
-      const int32_t x = tid >= w ? sa[tid - w] : 0;
-      const int32_t y = both && tid >= w ? sb[tid - w] : 0;
-      __syncthreads();
-      sa[tid] += x;
-      if (both) sb[tid] += y;
-      __syncthreads();
-    }
-  };
+  const int tid = threadIdx.x;
   int32_t carry_seg = 0, carry_scr = 0, carry_split = 0;
   for (int64_t base = 0; base < n_blocks; base += 1024) {
     const int64_t p = base + tid;
@@ -485,13 +491,9 @@ seg_build_kernel(const int32_t* __restrict__ col_nnz, const int32_t* __restrict_
       nseg = static_cast<int32_t>(k < 1 ? 1 : (k > max_seg ? max_seg : k));
     }
     const int32_t nscr = nseg > 1 ? nseg : 0;
-    sa[tid] = nseg;
-    sb[tid] = nscr;
-    __syncthreads();
-    scan(true);
-    const int32_t first = carry_seg + sa[tid] - nseg;
-    const int32_t first_scr = carry_scr + sb[tid] - nscr;
-    const int32_t tot_seg = sa[1023], tot_scr = sb[1023];
+    int32_t tot_seg, tot_scr, tot_split;
+    const int32_t first = carry_seg + block_scan_1024(nseg, wtot, tot_seg) - nseg;
+    const int32_t first_scr = carry_scr + block_scan_1024(nscr, wtot, tot_scr) - nscr;
     for (int32_t j = 0; j < nseg; ++j) {
       const int64_t at = first + j;
       if (at < cap) {
@@ -502,14 +504,9 @@ seg_build_kernel(const int32_t* __restrict__ col_nnz, const int32_t* __restrict_
         e[3] = nscr ? first_scr + j : -1;
       }
     }
-    __syncthreads();  // every thread has read the scans
-    sa[tid] = nscr ? 1 : 0;
-    __syncthreads();
-    scan(false);
-    if (nscr && carry_split + sa[tid] - 1 < extra_cap)
-      split[rh * extra_cap + carry_split + sa[tid] - 1] = first;
-    const int32_t tot_split = sa[1023];
-    __syncthreads();
+    const int32_t nth = block_scan_1024(nscr ? 1 : 0, wtot, tot_split);  // cut columns so far
+    if (nscr && carry_split + nth - 1 < extra_cap)
+      split[rh * extra_cap + carry_split + nth - 1] = first;
     carry_seg += tot_seg;
     carry_scr += tot_scr;
     carry_split += tot_split;
