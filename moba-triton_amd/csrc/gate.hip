@@ -95,28 +95,42 @@ gate_prep_kernel(const T* __restrict__ kbar, const int32_t* __restrict__ cu,
   // Eight lanes per block of kbar, each summing every eighth feature; the
   // partial sums meet by shuffles (the bound these norms feed carries a
   // 1e-4 relative slack, far above any float summation order's effect).
+  // A grid-stride loop over the blocks, the maximum taken within the
+  // workgroup, then one device atomic per workgroup (a few per row instead
+  // of one per wave, which serialised on the row's word).
+  __shared__ unsigned s_best[4];
   const int64_t rh = blockIdx.y;
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t j = gid >> 3;
-  const int sub = static_cast<int>(gid & 7);
+  const int sub = static_cast<int>(threadIdx.x & 7);
   // Only the blocks a sequence owns hold data; the tail of a packed kbar row
   // is never read by the gate.
   const SeqSpan sp = seq_span(cu, rh / h_kv, S);
   const int64_t owned = (sp.len + bs - 1) / bs < n_blocks ? (sp.len + bs - 1) / bs : n_blocks;
-  float ss = 0.f;
-  if (j < owned) {
-    const T* row = kbar + (rh * n_blocks + j) * D;
-    for (int64_t d = sub; d < D; d += 8) {
-      const float x = Elem<T>::load(row, d);
-      ss = fmaf(x, x, ss);
+  unsigned best = 0u;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * (blockDim.x >> 3);
+  // Every lane of an 8-lane group runs the same trips, so the shuffles below
+  // see all eight.
+  for (int64_t j = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 3;
+       j - (threadIdx.x >> 3) < owned; j += stride) {
+    float ss = 0.f;
+    if (j < owned) {
+      const T* row = kbar + (rh * n_blocks + j) * D;
+      for (int64_t d = sub; d < D; d += 8) {
+        const float x = Elem<T>::load(row, d);
+        ss = fmaf(x, x, ss);
+      }
     }
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    if (j < owned) best = max(best, f2u(sqrtf(ss)) & 0x7fffffffu);  // drop the sign of a NaN
   }
-  ss += __shfl_xor(ss, 1);
-  ss += __shfl_xor(ss, 2);
-  ss += __shfl_xor(ss, 4);
-  unsigned best = j < owned ? f2u(sqrtf(ss)) & 0x7fffffffu : 0u;  // drop the sign of a NaN
   for (int off = 32; off > 0; off >>= 1) best = max(best, static_cast<unsigned>(__shfl_xor(static_cast<int>(best), off)));
-  if ((threadIdx.x & 63) == 0 && best != 0u) atomicMax(norm_bits + rh, best);
+  if ((threadIdx.x & 63) == 0) s_best[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    best = max(max(s_best[0], s_best[1]), max(s_best[2], s_best[3]));
+    if (best != 0u) atomicMax(norm_bits + rh, best);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1022,7 +1036,7 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   hipLaunchKernelGGL(gate_init_kernel, dim3(1), dim3(256), 0, st, norm_bits,
                      g.rows * g.h_kv, ws.counter);
   hipLaunchKernelGGL(gate_prep_kernel<T>,
-                     dim3(static_cast<unsigned>(cdiv(g.n_blocks * 8, 256)),
+                     dim3(static_cast<unsigned>(cdiv(g.n_blocks * 8, 256) < 16 ? cdiv(g.n_blocks * 8, 256) : 16),
                           static_cast<unsigned>(g.rows * g.h_kv)),
                      dim3(256), 0, st, static_cast<const T*>(kbar), cu, g.seq_len,
                      g.h_kv, g.n_blocks, g.head_dim, g.block_size, norm_bits);
