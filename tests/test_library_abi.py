@@ -56,9 +56,12 @@ def test_invalid_arguments_fail_on_the_host():
 def test_workspace_queries_are_host_only():
     lib = _lib.load()
     assert lib.moba_gate_workspace_size(1, 65536, 4) >= 8 * 65536 * 4
-    # count table: 4 heads x 64 tiles x 512 columns; chunk sums: 4 kv heads x
-    # 4 chunks (64 units in chunks of 16) x 512 columns
-    assert lib.moba_csc_workspace_size(1, 65536, 4, 4, 512, 8) == 4 * (4 * 64 + 4 * 4) * 512
+    # 1024-query tiles would give 4 x 64 = 256 units (< 512), so the build
+    # takes 256-query tiles. Count table: 4 heads x 256 tiles x 512 columns;
+    # chunk sums: 4 kv heads x 16 chunks (256 units in chunks of 16) x 512.
+    assert lib.moba_csc_workspace_size(1, 65536, 4, 4, 512, 8) == 4 * (4 * 256 + 4 * 16) * 512
+    # 512K: 4 x 512 units at 1024 queries each. Chunk sums: 32 chunks of 16.
+    assert lib.moba_csc_workspace_size(1, 524288, 4, 4, 4096, 8) == 4 * (4 * 512 + 4 * 32) * 4096
     # past 16384 columns: the table of one 16384-column window
     tiles = (1 << 22) // 1024
     chunk = -(-2 * tiles // 64)
