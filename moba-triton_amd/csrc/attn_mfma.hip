@@ -483,7 +483,7 @@ bwd_mfma_kernel(AttnArgs a) {
   uint16_t* DSt = Os + NQ * RS;
   uint16_t* Kt = Kl;          // one stream
   uint16_t* Ks = Kl;          // two streams
-  uint16_t* Vs = Kl + BS * RS;
+  uint16_t* Vs = kKV ? Kl + BS * RS : Kl;  // (unused with one stream)
   float* s_lse = s_lse_[stream];
   float* s_delta = s_delta_[stream];
   int* s_lim = s_lim_[stream];
