@@ -145,3 +145,18 @@ def test_gate_every_score_a_candidate(device, d):
     idx = check(q, k, cfg)
     last = idx[0, 0, -1].tolist()  # the last query: own block 63, top 7 of 0..62
     assert last == list(range(56, 64)), last
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_gate_overflowing_scores_tie_to_the_lowest_blocks(device, d):
+    """q and k near 1e19: every dot product exceeds float32's range, so every
+    score is +inf and every strictly-past block ties. The gate cannot bound
+    such scores and sends the queries to its exact queue kernel, whose
+    selection must be the oracle's: the lowest block ids."""
+    cfg = MoBAConfig(block_size=128, top_k=8)
+    S = 2048
+    q = torch.full((1, S, 2, d), 1e19, dtype=torch.bfloat16, device=device)
+    k = torch.full((1, S, 2, d), 1e19, dtype=torch.bfloat16, device=device)
+    idx = check(q, k, cfg)
+    last = idx[0, 0, -1].tolist()  # own block 15, the 7 lowest past blocks
+    assert last == [0, 1, 2, 3, 4, 5, 6, 15], last
