@@ -342,36 +342,32 @@ gate_exact_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 }
 
 // ---------------------------------------------------------------------------
-// Queue kernel: one wave per queued query. Lanes split the candidates, keep
-// exact top-T lists, and merge them with a butterfly over the wave.
+// Queue kernel: one wave per queued query, four queries per workgroup. The
+// lanes split the query's candidates, each keeps an exact top-T list, and
+// the lists merge with a butterfly over the wave. Queries reach the queue
+// when the MFMA kernel's evidence cannot settle them: rarely for
+// independent keys, by the thousands for keys whose representatives nearly
+// coincide (many equal rounded scores), so the kernel is laid out for
+// throughput: no workgroup barriers, and each lane requests the rows of U
+// blocks before it scores any of them (float64 products and sum, as
+// exact_score), with the query row in registers.
 // ---------------------------------------------------------------------------
-// Lanes per queued query (8 waves: 256 registers each).
-template <typename T> constexpr int queue_threads() { return 512; }
+constexpr int kQueueWaves = 4;
+
 template <typename T, int TMAX, int D>
-__global__ void __launch_bounds__(queue_threads<T>())
+__global__ void __launch_bounds__(64 * kQueueWaves)
 gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                   int32_t* __restrict__ out, const int32_t* __restrict__ cu,
                   int64_t S, int64_t rows_per_seq, int64_t h_q, int64_t h_kv,
                   int64_t n_blocks, int bs, int take, int cur, int slots,
                   const int64_t* __restrict__ queue, const int* __restrict__ queue_len) {
-  // One workgroup per queued query: its lanes split the candidates, each
-  // keeps an exact top-T list, the lists merge with a butterfly inside each
-  // wave and then across the waves through LDS. A queued query is rare,
-  // so its time is the latency of one workgroup, set by the memory round
-  // trips of its candidate loop: the query row sits in registers and each
-  // lane requests the rows of U blocks before it scores any of them
-  // (float64 products and sum, as exact_score): at head_dim 64, 4096
-  // candidates take 2 round trips.
   constexpr int U = 256 / D;  // rows in flight per lane
   constexpr int C = D / 8;     // 16-byte chunks per row
-  constexpr int NWQ = queue_threads<T>() / 64;
-  __shared__ float s_v[NWQ][TMAX];
-  __shared__ int s_i[NWQ][TMAX];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int64_t total = *queue_len;
   const bool packed = cu != nullptr;
-  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kQueueWaves + (threadIdx.x >> 6);
+  for (int64_t item = first; item < total; item += static_cast<int64_t>(gridDim.x) * kQueueWaves) {
     const int64_t code = queue[item];  // (r * h_q + hq) * rows_per_seq + t
     const int64_t t = code % rows_per_seq;
     const int64_t rh = code / rows_per_seq;
@@ -388,7 +384,7 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     if constexpr (Elem<T>::kCode == MOBA_FP16) {
       // fp16's software conversion needs the registers: one candidate at a
       // time per lane.
-      for (int j = threadIdx.x; j < own; j += blockDim.x) {
+      for (int j = lane; j < own; j += 64) {
         const float sc = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
         if (ranks_before(sc, j, val[take - 1], idx[take - 1])) insert_exact<TMAX>(val, idx, sc, j);
       }
@@ -396,18 +392,18 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       uint4 qv[C];
 #pragma unroll
       for (int c = 0; c < C; ++c) qv[c] = *reinterpret_cast<const uint4*>(qrow + 8 * c);
-      for (int j0 = threadIdx.x; j0 < own; j0 += U * blockDim.x) {
+      for (int j0 = lane; j0 < own; j0 += U * 64) {
         uint4 kv[U][C];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int j = j0 + u * blockDim.x;
+          const int j = j0 + u * 64;
           const T* krow = kb + static_cast<int64_t>(j < own ? j : 0) * D;
 #pragma unroll
           for (int c = 0; c < C; ++c) kv[u][c] = *reinterpret_cast<const uint4*>(krow + 8 * c);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int j = j0 + u * blockDim.x;
+          const int j = j0 + u * 64;
           double acc = 0.0;
 #pragma unroll
           for (int c = 0; c < C; ++c) {
@@ -427,43 +423,25 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
         }
       }
     }
-    // Each wave's lists meet by a butterfly of merges, then the waves'
-    // lists by a butterfly over the first NWQ lanes of wave 0.
-    auto butterfly = [&](int from) {
-      for (int off = from; off > 0; off >>= 1) {
-        float pv[TMAX];
-        int pi[TMAX];
 #pragma unroll
-        for (int p = 0; p < TMAX; ++p) {
-          pv[p] = __shfl_xor(val[p], off);
-          pi[p] = __shfl_xor(idx[p], off);
-        }
-        merge_top<TMAX>(val, idx, pv, pi);
-      }
-    };
-    butterfly(32);
-    if (lane == 0) {
-#pragma unroll
-      for (int p = 0; p < TMAX; ++p) { s_v[wave][p] = val[p]; s_i[wave][p] = idx[p]; }
-    }
-    __syncthreads();
-    if (wave == 0) {
+    for (int off = 32; off > 0; off >>= 1) {
+      float pv[TMAX];
+      int pi[TMAX];
 #pragma unroll
       for (int p = 0; p < TMAX; ++p) {
-        val[p] = lane < NWQ ? s_v[lane][p] : -INFINITY;
-        idx[p] = lane < NWQ ? s_i[lane][p] : 0x7fffffff;
+        pv[p] = __shfl_xor(val[p], off);
+        pi[p] = __shfl_xor(idx[p], off);
       }
-      butterfly(NWQ / 2);
-      if (lane == 0) {
-        int n_sel = 0;
-#pragma unroll
-        for (int p = 0; p < TMAX; ++p)
-          if (p < take && val[p] > -INFINITY) n_sel = p + 1;
-        emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
-                          out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
-      }
+      merge_top<TMAX>(val, idx, pv, pi);
     }
-    __syncthreads();
+    if (lane == 0) {
+      int n_sel = 0;
+#pragma unroll
+      for (int p = 0; p < TMAX; ++p)
+        if (p < take && val[p] > -INFINITY) n_sel = p + 1;
+      emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
+                        out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
+    }
   }
 }
 
@@ -509,6 +487,7 @@ __device__ inline void insert_value(float (&l)[K], float x) {
   for (int p = K - 1; p > 0; --p) l[p] = __builtin_amdgcn_fmed3f(l[p - 1], l[p], x);
   l[0] = fmaxf(l[0], x);
 }
+
 template <typename T, int D, int M, int K, int CAP, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64, (D == 64 && M <= 12) ? 3 : 1)
 gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
@@ -771,9 +750,18 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
 
   // --- Merge the two half-lists of this query and decide. -----------------
-  // Every approximate score a carries |a - exact| <= E. Scores >= theta left
-  // out of a lane's list are <= its M-th (rej; none while the list is not
-  // full); scores below theta never entered.
+  // A query's ranking key is its exact score rounded to float32 and then to
+  // the storage dtype (ties broken by the lower id). Every approximate
+  // score a carries |a - exact| <= E, so its key lies in
+  // [R(a - w), R(a + w)] (R: that rounding, monotone; w: E widened by the
+  // float32 rounding of a -+ E). Keys are coarse (one dtype ulp is far
+  // wider than E), so most intervals are a single key: those candidates
+  // are ranked as they are, and only the ones whose interval straddles a
+  // rounding boundary are rescored exactly. Candidates left out of the
+  // lists scored below theta, or at most a lane's M-th entry (rej; none
+  // while the list is not full): their keys are at most R(U + w(U)) with U
+  // the larger of the two, and the result stands when that is below the
+  // take-th selected key.
   const float rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
   const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
   float pv[M];
@@ -783,61 +771,47 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     pv[p] = __shfl_xor(lv[p], 32);
     pi[p] = __shfl_xor(li[p], 32);
   }
-  // L: the take-th approximate score of the union; N: the (take + 1)-th.
+  auto widen = [&](float a) { return E * 1.001f + fabsf(a) * 2.4e-7f; };  // 2.4e-7 > 2^-22
+  // L: the take-th approximate score of the union. At least `take` listed
+  // candidates have keys >= Lk; one whose key interval ends below Lk is
+  // outranked by all of them.
   const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
-  const float N = take > 0 ? kth_of_union<M>(lv, pv, take + 1) : -INFINITY;
-  bool ok = true;
-  float cut = -INFINITY;
-  if (take > 0 && L > -INFINITY) {
-    const float mag = band_mag(L);
-    if (!(mag < Ops::kMaxFinite)) ok = false;
-    if (rej > -INFINITY && !(L - rej > band_at(fmaxf(mag, band_mag(rej))))) ok = false;
-    cut = L - band_at(mag);
-    if (!(cut >= theta)) ok = false;  // a needed candidate may lie below theta
-  }
-  // q or kbar carries inf / NaN, or a float32 score could overflow.
-  if (take > 0 && !(qnorm * knorm < 3.0e38f)) ok = false;
+  const float Lk = L > -INFINITY ? Elem<T>::round(L - widen(L)) : -INFINITY;
+  // q or kbar carries inf / NaN, or a score could round to an infinite key.
+  bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
 
-  // Union entries >= cut: those that surely outrank the (take + 1)-th score
-  // (and so everything from there down) are selected outright; the rest
-  // are rescored exactly (float64) by the two lanes together, each forming
-  // the partial dot over the features it holds, and ranked by (score desc,
-  // id asc). Both lanes walk the union in the same order (half 0's list
-  // first) and reach identical results. Outright ids collect in a per-lane
-  // LDS list in the (now idle) kbar staging buffer, uncertain ids in the
-  // lane's candidate buffer.
+  // The candidates that can still rank in the top `take`, with exact keys,
+  // in (key desc, id asc) order. Both lanes walk the union in the same
+  // order (half 0's list first) and reach identical lists; uncertain ids
+  // wait in the lane's candidate buffer and are rescored (float64) by the
+  // two lanes together, each forming the partial dot over the features it
+  // holds.
   constexpr int TS = M <= 12 ? 8 : 16;  // most past blocks one query selects
-  uint32_t* ss = reinterpret_cast<uint32_t*>(&s_kb[0][0]) + wave * TS * 64 + lane;
   float fv[TS];
   int fi[TS];
 #pragma unroll
   for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
-  int ns = 0;
   uint32_t* su = reinterpret_cast<uint32_t*>(sv);
   if (ok && take > 0 && live) {
-    const float hiN = N > -INFINITY ? N + E : -INFINITY;
     int nu = 0;
-#pragma unroll
-    for (int p = 0; p < 2 * M; ++p) {
-      const bool own_list = (p < M) == (half == 0);
-      const float x = own_list ? lv[p % M] : pv[p % M];
-      const int j = own_list ? li[p % M] : pi[p % M];
-      if (!(x > -INFINITY && x >= cut)) continue;
-      bool sure = !(N > -INFINITY);
-      if (!sure) {
-        const float lo = x - E;
-        const float mi = fmaxf(fabsf(x) + E, fabsf(hiN));
-        sure = lo - hiN > Ops::kGapRel * mi + Ops::kGapAbs;
-      }
-      if (sure) {
-        ss[ns * 64] = static_cast<uint32_t>(j);
-        ++ns;
+    auto visit = [&](float x, int j) {
+      if (!(x > -INFINITY)) return;
+      const float w = widen(x);
+      const float khi = Elem<T>::round(x + w);
+      if (khi < Lk) return;
+      const float klo = Elem<T>::round(x - w);
+      if (klo == khi) {
+        insert_exact<TS>(fv, fi, klo, j);
       } else {
         if (nu < CAP) su[nu * 64] = static_cast<uint32_t>(j);
         ++nu;
       }
-    }
-    if (nu > CAP) ok = false;  // more near-ties than the buffer holds
+    };
+#pragma unroll
+    for (int p = 0; p < M; ++p) visit(half == 0 ? lv[p] : pv[p], half == 0 ? li[p] : pi[p]);
+#pragma unroll
+    for (int p = 0; p < M; ++p) visit(half == 0 ? pv[p] : lv[p], half == 0 ? pi[p] : li[p]);
+    if (nu > CAP) ok = false;  // more straddling candidates than the buffer holds
     constexpr int R = 2;
 #pragma unroll 1
     for (int u0 = 0; ok && u0 < nu; u0 += R) {
@@ -865,6 +839,15 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
         if (u0 + r < nu && sc > -INFINITY) insert_exact<TS>(fv, fi, sc, jr[r]);
       }
     }
+    // Candidates outside the lists must rank below the take-th selected.
+    const float U = fmaxf(rej, theta);
+    if (U > -INFINITY) {
+      const float Uk = Elem<T>::round(U + widen(U));
+      float kt = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
+      if (!(kt > Uk)) ok = false;
+    }
   }
   if (!live || half != 0) return;
   const int64_t qid = hm_query(packed, r, hq, h_q, S, tok, t);
@@ -873,17 +856,14 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     queue[slot] = (r * h_q + hq) * rows_per_seq + t;
     return;
   }
-  // Selected: the outright ids, then the best (take - ns) rescored ones.
-  int n_sel = ns;
-#pragma unroll
-  for (int p = 0; p < TS; ++p)
-    if (p < take - ns && fv[p] > -INFINITY) {
-      ss[(ns + p) * 64] = static_cast<uint32_t>(fi[p]);
-      n_sel = ns + p + 1;
-    }
+  int n_sel = 0;
   int sel[TS];
 #pragma unroll
-  for (int p = 0; p < TS; ++p) sel[p] = p < n_sel ? static_cast<int>(ss[p * 64]) : 0x7fffffff;
+  for (int p = 0; p < TS; ++p) {
+    const bool in = p < take && fv[p] > -INFINITY;
+    sel[p] = in ? fi[p] : 0x7fffffff;
+    n_sel += in ? 1 : 0;
+  }
   emit_sorted<TS>(sel, n_sel, own, cur != 0, out + qid * slots, slots);
 }
 
@@ -921,8 +901,9 @@ gate_refine_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     const int c = lane + 64 * u;
     if (c >= n_cand) break;
     const int sb = sp[c / group];
+    if (sb < 0 || sb > (n_blocks - 1) / group) continue;  // no block (and no overflow)
     const int j = sb * group + c % group;
-    if (sb < 0 || j >= own || j >= n_blocks) continue;
+    if (j >= own || j >= n_blocks) continue;
     insert_exact<LMAX>(val, idx, exact_score(qrow, kb + static_cast<int64_t>(j) * D, D), j);
   }
   int sel[TMAX];
@@ -1053,7 +1034,7 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   // Queries whose approximate evidence was insufficient: exact rescoring,
   // one wave per query.
   auto queue_launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, dim3(512), dim3(queue_threads<T>()), 0, st, static_cast<const T*>(q),
+    hipLaunchKernelGGL(kernel, dim3(1024), dim3(64 * kQueueWaves), 0, st, static_cast<const T*>(q),
                        static_cast<const T*>(kbar), out, cu, g.seq_len, g.rows_per_seq, g.h_q,
                        g.h_kv, g.n_blocks, static_cast<int>(g.block_size), take, cur,
                        static_cast<int>(g.slots), ws.queue, ws.counter);

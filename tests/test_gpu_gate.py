@@ -160,3 +160,29 @@ def test_gate_overflowing_scores_tie_to_the_lowest_blocks(device, d):
     idx = check(q, k, cfg)
     last = idx[0, 0, -1].tolist()  # own block 15, the 7 lowest past blocks
     assert last == [0, 1, 2, 3, 4, 5, 6, 15], last
+
+
+def _structured_keys(kind, shape, dtype, seed, device):
+    """Keys whose block representatives nearly coincide, so that many scores
+    round to equal values of the storage dtype: a shared per-channel offset
+    plus noise ("bias", as trained keys carry), or a slow random walk over
+    the tokens ("walk")."""
+    g = torch.Generator().manual_seed(seed)
+    if kind == "bias":
+        k = 3.0 * torch.randn((1, 1) + tuple(shape[2:]), generator=g) + torch.randn(shape, generator=g)
+    else:
+        k = (torch.randn(shape, generator=g) * 0.05).cumsum(1)
+    return k.to(dtype).to(device)
+
+
+@pytest.mark.parametrize("kind", ["bias", "walk"])
+@pytest.mark.parametrize("d,gate", [(64, (64, 8)), (128, (64, 8)), (64, (32, 17)), (128, (128, 12))])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gate_near_tied_keys_match_oracle(device, kind, d, gate, dtype):
+    """Many candidates share a rounded score: the order among them is the
+    block id, which the gate must reproduce exactly."""
+    cfg = MoBAConfig(block_size=gate[0], top_k=gate[1], dtype=dtype)
+    shape = (1, 8192, 2, d)
+    q = make_qkv(shape, dtype, seed=31, device=device, n=1)[0]
+    k = _structured_keys(kind, shape, dtype, 32, device)
+    check(q, k, cfg)

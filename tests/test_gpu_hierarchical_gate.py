@@ -81,3 +81,24 @@ def test_hierarchical_gate_in_attention_and_packed_rejected(device):
     cu = torch.tensor([0, 1024, 2048], dtype=torch.int32, device=device)
     with pytest.raises(ValueError, match="padded input only"):
         moba_attention(q, k, v, cfg, cu_seqlens=cu, max_seqlen=1024)
+
+
+def test_refine_ignores_super_block_ids_that_hold_no_block(device):
+    """Ids past the last super-block (here large enough that id * group
+    overflows int32) and negative ids other than -1 select nothing: each
+    query keeps only its own block."""
+    from moba import _lib
+
+    b, s, h, d, bs, group = 1, 1024, 2, 64, 64, 4
+    q, k, _ = make_qkv((b, s, h, d), torch.bfloat16, seed=33, device=device)
+    kbar = pool_blocks(k, MoBAConfig(bs, 4))
+    sup = torch.tensor([1 << 30, -5, 4], dtype=torch.int32, device=device).expand(b, h, s, 3)
+    sup = sup.contiguous()
+    out = torch.full((b, h, s, 4), -7, dtype=torch.int32, device=device)
+    _lib.call("moba_gate_refine", _lib.ptr(q), _lib.ptr(kbar), _lib.ptr(sup), _lib.ptr(out), b, s,
+              h, h, d, s // bs, bs, group, 3, 4, 3, 1, _lib.DTYPE_CODE[q.dtype],
+              _lib.stream_handle(device))
+    got = out.cpu()
+    own = (torch.arange(s) // bs).view(1, 1, s).expand(b, h, s)
+    assert torch.equal(got[..., 0], own)
+    assert bool((got[..., 1:] == -1).all())
