@@ -24,21 +24,23 @@
 //     its block id to a per-lane LDS buffer, folding it into a sorted list
 //     of the M best when it may overflow (the threshold then rises to the
 //     M-th).
-//   - Decide: the pair merges its lists (k-th of union: L = take-th,
-//     N = (take + 1)-th, rej = the larger M-th). |approx - exact| <= E with
-//     E = 2^-14 |q| max|kbar| plus the denormal terms (any float32 sum of D
-//     <= 128 products is within D 2^-24 |q| |kbar|); band = 2E + a 2^-7
-//     relative gap, so two scores further apart than the band round to
-//     distinct bf16/fp16 values in the same order. The query is decidable
-//     when L - rej and L - theta exceed the band and nothing overflows.
-//     Entries that surely outrank N are selected outright; the others
-//     within the band of L are rescored exactly (float64 partial dots of the
-//     two lanes, rounded like the oracle) and ranked by (score desc, id asc).
-//   A query that is not decidable (near-ties beyond the lists, constructed
-//   ties, inf / NaN input) is queued; it is never guessed.
+//   - Decide: |approx - exact| <= E with E = 2^-14 |q| max|kbar| plus the
+//     denormal terms (any float32 sum of D <= 128 products is within
+//     D 2^-24 |q| |kbar|), so a score's key (the exact score rounded to
+//     float32 and to the dtype) lies in [R(a - w), R(a + w)], w being E
+//     widened by float32 rounding. Candidates whose interval ends below the
+//     key floor of the pair's take-th score cannot rank; of the rest, those
+//     with a single possible key are ranked by it, and those straddling a
+//     rounding boundary are rescored exactly (float64 partial dots of the
+//     two lanes, rounded like the oracle). The result stands when every
+//     candidate left out of the lists (below theta, or at most the larger
+//     M-th entry) has a key bound strictly below the take-th selected key.
+//   A query that the lists cannot settle (more equal keys at the boundary
+//   than they hold, constructed ties, inf / NaN input) is queued; it is
+//   never guessed.
 //
-// * gate_queue_kernel: one workgroup per queued query, exact scores for
-//   every candidate, lists merged across the workgroup.
+// * gate_queue_kernel: one wave per queued query, exact scores for every
+//   candidate, lists merged across the wave.
 //
 // * gate_exact_kernel (fp32, take > 16 or unsupported shapes). One thread
 //   per query, exact float64 scores for every candidate, streaming top-T in
