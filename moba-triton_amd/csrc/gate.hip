@@ -19,7 +19,8 @@
 //   - Pass 1 keeps, per lane, the K largest chunk maxima. The take-th
 //     largest of the pair's union is the take-th best of a subset of the
 //     query's candidates, hence a lower bound on L (the take-th best of
-//     all); theta = that bound - band.
+//     all); theta lies just below the scores that can round to the key
+//     R(bound - w) or above (every selected key is at least that).
 //   - Pass 2 appends every score above the lane's threshold (>= theta) with
 //     its block id to a per-lane LDS buffer, folding it into a sorted list
 //     of the M best when it may overflow (the threshold then rises to the
@@ -456,10 +457,6 @@ template <> struct MfmaOps<bf16_t> {
   __device__ static floatx16_t mfma(vec a, vec b, floatx16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // Two values more than one bf16 ulp apart (<= 2^-7 relative) can never
-  // round to the same bf16 value; 1% slack on top.
-  static constexpr float kGapRel = 0.0078125f * 1.01f;
-  static constexpr float kGapAbs = 1e-30f;
   static constexpr float kMaxFinite = 3.0e38f;
   // Largest magnitude the MFMA may flush as a denormal input.
   static constexpr float kDenorm = 1.2e-38f;
@@ -469,11 +466,20 @@ template <> struct MfmaOps<f16_t> {
   __device__ static floatx16_t mfma(vec a, vec b, floatx16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static constexpr float kGapRel = 0.0078125f * 1.01f;  // covers fp16's 2^-10 ulps
-  static constexpr float kGapAbs = 2.0e-7f;    // > 2 fp16 subnormal spacings
   static constexpr float kMaxFinite = 60000.f;  // beyond: fp16 rounds to inf
   static constexpr float kDenorm = 6.2e-5f;     // fp16 subnormals are below 2^-14
 };
+
+// The next value of T's format below v (v itself a finite value of it).
+template <typename T> __device__ inline float key_below(float v);
+template <> __device__ inline float key_below<bf16_t>(float v) {
+  const uint16_t b = float_to_bf16(v);
+  return bf16_to_float(v > 0.f ? b - 1 : (v < 0.f ? b + 1 : 0x8001));
+}
+template <> __device__ inline float key_below<f16_t>(float v) {
+  const uint16_t b = float_to_f16(v);
+  return f16_to_float(v > 0.f ? b - 1 : (v < 0.f ? b + 1 : 0x8001));
+}
 
 template <typename V>
 __device__ inline V load_vec16(const void* p) {
@@ -560,13 +566,8 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Slack for the float sum of squares and sqrtf (a few ulp).
   const float knorm = kbar_norm[r * h_kv + hk] * 1.0001f + 1e-30f;
   const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
-  // Decision band around a key value x: two scores whose keys lie more than
-  // band(x) apart (magnitudes <= band_mag(x)) round to distinct values of
-  // the storage dtype, in key order. band_mag also covers the magnitude of
-  // x - band(x) itself.
-  auto band_mag = [&](float x) { return (fabsf(x) + 2.f * E) * 1.05f + 2.f * Ops::kGapAbs; };
-  auto band_at = [&](float m) { return 2.f * E + Ops::kGapRel * (m + E) + Ops::kGapAbs; };
-  auto band = [&](float x) { return band_at(band_mag(x)); };
+  // E widened by the float32 rounding of a -+ E (2.4e-7 > 2^-22).
+  auto widen = [&](float a) { return E * 1.001f + fabsf(a) * 2.4e-7f; };
 
   const int n_chunks = (take > 0 && hz > 0) ? (hz + 31) / 32 : 0;
   const int n_stages = (n_chunks + 1) / 2;
@@ -602,7 +603,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // the two lanes' lists is the take-th best of a subset of the query's
   // candidates, so it is <= L (the take-th best of all of them); with the
   // top blocks spread over chunks it is L itself. Every candidate that can
-  // matter then scores >= theta = (that value) - band - key slack.
+  // matter then has a key >= R(that value - w) and a score >= theta.
   // Lane 0 of the wave holds its smallest query, so its own block bounds
   // every lane's: chunks entirely below it need no causal mask.
   const int own_min = __builtin_amdgcn_readfirstlane(own);
@@ -667,13 +668,20 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 #pragma unroll
     for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
     const float tau = kth_of_union<K>(tk, pk, take);
-    if (tau > -INFINITY) theta = tau - band(tau);
+    // Keys of the take-th best and above are >= kt0 = R(tau - w); scores
+    // below the midpoint between kt0 and the key under it (less a margin
+    // of two widths) round below kt0 and cannot be needed.
+    if (tau > -INFINITY) {
+      const float kt0 = Elem<T>::round(tau - widen(tau));
+      const float mid = 0.5f * (kt0 + key_below<T>(kt0));
+      theta = nextafterf(mid - 2.f * widen(mid), -INFINITY);
+    }
   }
   // Collection threshold: a > thr0 is a >= theta.
   const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
   // --- Pass 2: every chunk again. Each score above the lane's threshold
-  // (rare: theta sits within the decision band of L) is appended, with its
+  // (rare: theta sits about one key below L) is appended, with its
   // block id, to the lane's LDS buffer; a buffer that may overflow on the
   // next chunk is folded into the lane's list of its M best scores (value
   // order; ties are settled by the exact rescoring), and the threshold
@@ -773,7 +781,6 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     pv[p] = __shfl_xor(lv[p], 32);
     pi[p] = __shfl_xor(li[p], 32);
   }
-  auto widen = [&](float a) { return E * 1.001f + fabsf(a) * 2.4e-7f; };  // 2.4e-7 > 2^-22
   // L: the take-th approximate score of the union. At least `take` listed
   // candidates have keys >= Lk; one whose key interval ends below Lk is
   // outranked by all of them.
