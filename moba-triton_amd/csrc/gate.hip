@@ -565,7 +565,10 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   const float qnorm = sqrtf(qn) * 1.0001f;
   // Slack for the float sum of squares and sqrtf (a few ulp).
   const float knorm = kbar_norm[r * h_kv + hk] * 1.0001f + 1e-30f;
-  const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) + 1e-37f;
+  // The last term covers float32 denormal products or partial sums the
+  // matrix core may flush: at most 2^-126 each, D + 1 of them.
+  const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) +
+                  (D + 1) * 1.2e-38f;
   // E widened by the float32 rounding of a -+ E (2.4e-7 > 2^-22).
   auto widen = [&](float a) { return E * 1.001f + fabsf(a) * 2.4e-7f; };
 

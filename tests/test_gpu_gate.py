@@ -186,3 +186,30 @@ def test_gate_near_tied_keys_match_oracle(device, kind, d, gate, dtype):
     q = make_qkv(shape, dtype, seed=31, device=device, n=1)[0]
     k = _structured_keys(kind, shape, dtype, 32, device)
     check(q, k, cfg)
+
+
+@pytest.mark.parametrize("dtype,scale", [
+    (torch.bfloat16, 1e-19), (torch.bfloat16, 1e-12), (torch.bfloat16, 1e12),
+    (torch.float16, 0.02), (torch.float16, 20.0),
+])
+def test_gate_near_tied_keys_at_extreme_scales(device, dtype, scale):
+    """Offset keys scaled so that the scores sit among subnormal or very large
+    rounded values (the key intervals and the threshold below the bound then
+    meet the format's edges), and, for float16, near its overflow."""
+    cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
+    shape = (1, 4096, 2, 64)
+    q = (make_qkv(shape, torch.float32, seed=35, device=device, n=1)[0] * scale).to(dtype)
+    k = (_structured_keys("bias", shape, torch.float32, 36, device) * scale).to(dtype)
+    check(q, k, cfg)
+
+
+@pytest.mark.parametrize("kind", ["bias", "walk"])
+def test_gate_near_tied_keys_packed_gqa_match_oracle(device, kind):
+    """Near-tied keys through the packed path with grouped query heads."""
+    cfg = MoBAConfig(block_size=64, top_k=8, dtype=torch.bfloat16)
+    lens = [3000, 517, 4096, 1200]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    t = int(cu[-1])
+    q = make_qkv((1, t, 4, 64), torch.bfloat16, seed=37, device=device, n=1)[0]
+    k = _structured_keys(kind, (1, t, 2, 64), torch.bfloat16, 38, device)
+    check(q, k, cfg, cu.to(device), max(lens))
