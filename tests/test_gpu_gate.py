@@ -213,3 +213,35 @@ def test_gate_near_tied_keys_packed_gqa_match_oracle(device, kind):
     q = make_qkv((1, t, 4, 64), torch.bfloat16, seed=37, device=device, n=1)[0]
     k = _structured_keys(kind, (1, t, 2, 64), torch.bfloat16, 38, device)
     check(q, k, cfg, cu.to(device), max(lens))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gate_queue_settles_heavy_ties_exactly(device, dtype):
+    """Keys dominated by one shared offset: scores spread over only a few
+    rounded values, so the boundary key is shared by more candidates than
+    the MFMA kernel's lists hold. Those queries must reach the exact queue
+    kernel (its counter, the first word of the workspace, is non-zero) and
+    come out as the oracle selects them."""
+    from moba import _lib
+
+    cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
+    shape = (1, 8192, 2, 64)
+    g = torch.Generator().manual_seed(39)
+    scale = 1.0 if dtype is torch.bfloat16 else 0.25
+    q = (torch.randn(shape, generator=g) * scale).to(dtype).to(device)
+    k = ((8.0 * torch.randn((1, 1, 2, 64), generator=g) + torch.randn(shape, generator=g))
+         * scale).to(dtype).to(device)
+    kbar = pool_blocks(k, cfg)
+    b, s, h, d = q.shape
+    n = kbar.shape[2]
+    ws = torch.zeros(int(_lib.load().moba_gate_workspace_size(b, s, h)), dtype=torch.uint8,
+                     device=device)
+    out = torch.empty((b, h, s, cfg.slots()), dtype=torch.int32, device=device)
+    _lib.call("moba_gate", _lib.ptr(q), _lib.ptr(kbar), _lib.ptr(out), None, b, s, s, h, h, d, n,
+              cfg.block_size, cfg.slots(), cfg.past_blocks_selected(n), 1,
+              _lib.DTYPE_CODE[dtype], _lib.ptr(ws), ws.numel(), _lib.stream_handle(device))
+    queued = int(ws[:4].view(torch.int32)[0])
+    assert queued > 0, "no query reached the queue kernel"
+    ref = c_oracle.gate_select(q.cpu(), kbar.cpu(), oracle_cfg(cfg))
+    bad = (out.cpu() != ref).any(-1)
+    assert not bool(bad.any()), f"{int(bad.sum())} of {queued} queued queries differ"
