@@ -748,7 +748,7 @@ bwd_mfma_kernel(AttnArgs a) {
     }
     // dq[t][v] is feature 32dt + 8(v/4) + 4h + v%4 of query 32qt + col.
     if constexpr (sizeof(A) == 2) {
-      // Rows of dQ through LDS (Qs), then whole 16-byte chunks out.
+      // dQ through LDS (Qs): each wave its 32 x 32 tiles, 16-byte chunks out.
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int tt = wave + t * NW;
@@ -759,19 +759,30 @@ bwd_mfma_kernel(AttnArgs a) {
                     dq[t][4 * q4] * a.scale, dq[t][4 * q4 + 1] * a.scale,
                     dq[t][4 * q4 + 2] * a.scale, dq[t][4 * q4 + 3] * a.scale);
       }
-      __syncthreads();
+      // Each wave reads back only the 32 x 32 tiles it wrote (four 16-byte
+      // chunks per query and tile), so a wave-level barrier orders them; the
+      // next step's staging waits at the loop's first barrier. s_qoff, which
+      // derive() rewrites, was last read before the dS barrier.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (more) {
         c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
         derive();  // waits for every load in flight, before the stores
       }
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int i = stid + u * NT;
-        const int q = i / (D / 8);
-        const int d8 = (i % (D / 8)) * 8;
-        const int64_t dst = s_dst[q];
-        const u32x4 val = *reinterpret_cast<const u32x4*>(&Qs[q * RS + d8]);
-        if (dst >= 0) *reinterpret_cast<u32x4*>(dq_out + dst * D + d8) = val;
+      for (int t = 0; t < TPW; ++t) {
+        const int tt = wave + t * NW;
+        const int dt = tt % DT, qt = tt / DT;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int ci = lane + 64 * u;
+          const int q = qt * 32 + (ci >> 2);
+          const int d8 = dt * 32 + (ci & 3) * 8;
+          const int64_t dst = s_dst[q];
+          const u32x4 val = *reinterpret_cast<const u32x4*>(&Qs[q * RS + d8]);
+          if (dst >= 0) *reinterpret_cast<u32x4*>(dq_out + dst * D + d8) = val;
+        }
       }
     } else {
       if (more) {
