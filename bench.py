@@ -263,7 +263,11 @@ def hierarchical_gate(s, dev, configs=((16, 8), (4, 8)), reps=5):
     the share of the exact gate's strictly-past selections it keeps -- on the
     bench's i.i.d. keys (the worst case for any hierarchy) and on keys with
     positional locality (a random walk along the sequence plus unit noise),
-    the two cases of the reference's `docs/gate-hierarchical-measurements.md`."""
+    the two cases of the reference's `docs/gate-hierarchical-measurements.md`.
+    Also the exact gate's own time on those keys and on keys that share one
+    per-channel offset (3 offset + unit noise, as trained keys carry), whose
+    block representatives nearly coincide so that many scores tie once
+    rounded: `exact_gate_ms_by_keys`."""
     from moba.config import MoBAConfig
     from moba.kernels.gating import gate_select
     from moba.kernels.pooling import pool_blocks
@@ -275,6 +279,8 @@ def hierarchical_gate(s, dev, configs=((16, 8), (4, 8)), reps=5):
     walk = torch.randn(shape, generator=g, device=dev).mul_(0.05).cumsum_(1)
     k_walk = (walk + torch.randn(shape, generator=g, device=dev)).to(torch.bfloat16)
     del walk
+    k_offset = (3.0 * torch.randn((1, 1, HEADS, HEAD_DIM), generator=g, device=dev)
+                + torch.randn(shape, generator=g, device=dev)).to(torch.bfloat16)
     exact_cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
     own = (torch.arange(s, device=dev) // BLOCK).view(1, 1, s, 1)
 
@@ -287,6 +293,11 @@ def hierarchical_gate(s, dev, configs=((16, 8), (4, 8)), reps=5):
     exact = {n: gate_select(q, kb, exact_cfg) for n, kb in kbars.items()}
     out = {"exact_gate_ms": round(timed(lambda: gate_select(q, kbars["iid"], exact_cfg),
                                         reps, 1)[0], 4), "configs": []}
+    kb_offset = pool_blocks(k_offset, exact_cfg)
+    del k_offset
+    out["exact_gate_ms_by_keys"] = {
+        n: round(timed(lambda: gate_select(q, kb, exact_cfg), reps, 1)[0], 4)
+        for n, kb in (("iid", kbars["iid"]), ("walk", kbars["walk"]), ("offset", kb_offset))}
     for group, opened in configs:
         cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK, gate_group=group, gate_open=opened)
         row = {"gate_group": group, "gate_open": opened,

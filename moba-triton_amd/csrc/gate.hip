@@ -16,7 +16,7 @@
 //   tile per wave with the query on the lane axis, so each lane holds 16
 //   approximate float32 scores of its query per 32-block chunk and the
 //   bookkeeping never crosses lanes.
-//   - Pass 1 keeps, per lane, the K largest chunk maxima. The take-th
+//   - Pass 1 keeps, per lane, the K largest half-chunk maxima. The take-th
 //     largest of the pair's union is the take-th best of a subset of the
 //     query's candidates, hence a lower bound on L (the take-th best of
 //     all); theta lies just below the scores that can round to the key
@@ -600,9 +600,9 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     }
   };
 
-  // --- Pass 1: a lower bound on L from every chunk's maximum. ------------
-  // Each lane keeps the K largest of its per-chunk maxima (one score of one
-  // block each, all distinct blocks). The take-th largest of the union of
+  // --- Pass 1: a lower bound on L from every half-chunk's maximum. -------
+  // Each lane keeps the K largest of its per-half-chunk maxima (one score of
+  // one block each, all distinct blocks). The take-th largest of the union of
   // the two lanes' lists is the take-th best of a subset of the query's
   // candidates, so it is <= L (the take-th best of all of them); with the
   // top blocks spread over chunks it is L itself. Every candidate that can
@@ -653,19 +653,25 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     float tk[K];
 #pragma unroll
     for (int p = 0; p < K; ++p) tk[p] = -INFINITY;
+    // The maxima of the lane's two 8-block halves of each chunk: where the
+    // best blocks cluster (keys with locality), one maximum per chunk would
+    // leave the bound far below L and pass 2 would collect many more scores.
     stream_chunks([&](int ch, const floatx16_t& acc, bool full) {
-      float mx = -INFINITY;
-      if (full) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[v]);
-      } else {
+      for (int g = 0; g < 2; ++g) {
+        float mx = -INFINITY;
+        if (full) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-          mx = fmaxf(mx, b < own ? acc[v] : -INFINITY);
+          for (int v = 8 * g; v < 8 * g + 8; ++v) mx = fmaxf(mx, acc[v]);
+        } else {
+#pragma unroll
+          for (int v = 8 * g; v < 8 * g + 8; ++v) {
+            const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            mx = fmaxf(mx, b < own ? acc[v] : -INFINITY);
+          }
         }
+        insert_value<K>(tk, mx);
       }
-      insert_value<K>(tk, mx);
     });
     float pk[K];
 #pragma unroll
