@@ -16,29 +16,33 @@
 //   tile per wave with the query on the lane axis, so each lane holds 16
 //   approximate float32 scores of its query per 32-block chunk and the
 //   bookkeeping never crosses lanes.
-//   - Pass 1 keeps, per lane, the K largest half-chunk maxima. The take-th
-//     largest of the pair's union is the take-th best of a subset of the
-//     query's candidates, hence a lower bound on L (the take-th best of
-//     all); theta lies just below the scores that can round to the key
-//     R(bound - w) or above (every selected key is at least that).
-//   - Pass 2 appends every score above the lane's threshold (>= theta) with
-//     its block id to a per-lane LDS buffer, folding it into a sorted list
-//     of the M best when it may overflow (the threshold then rises to the
-//     M-th).
+//   - Pass 1 (every chunk once) keeps, per lane, the K largest maxima of
+//     its 4-block groups as keys that carry the group id and an LDS slot
+//     in their low mantissa bits, and each kept group's four scores in
+//     that slot. The take-th largest of the pair's kept maxima is the
+//     take-th best of a subset of the query's candidates, hence a lower
+//     bound on L (the take-th best of all); theta lies just below the
+//     scores that can round to the key R(bound - w) or above (every
+//     selected key is at least that).
 //   - Decide: |approx - exact| <= E with E = 2^-14 |q| max|kbar| plus the
 //     denormal terms (any float32 sum of D <= 128 products is within
 //     D 2^-24 |q| |kbar|), so a score's key (the exact score rounded to
 //     float32 and to the dtype) lies in [R(a - w), R(a + w)], w being E
-//     widened by float32 rounding. Candidates whose interval ends below the
-//     key floor of the pair's take-th score cannot rank; of the rest, those
-//     with a single possible key are ranked by it, and those straddling a
-//     rounding boundary are rescored exactly (float64 partial dots of the
-//     two lanes, rounded like the oracle). The result stands when every
-//     candidate left out of the lists (below theta, or at most the larger
-//     M-th entry) has a key bound strictly below the take-th selected key.
-//   A query that the lists cannot settle (more equal keys at the boundary
-//   than they hold, constructed ties, inf / NaN input) is queued; it is
-//   never guessed.
+//     widened by float32 rounding. The candidates (scores >= theta of the
+//     kept groups) are compacted per lane; those with a single possible
+//     key are ranked by it, those straddling a rounding boundary and not
+//     below the take-th lower key bound are rescored exactly (float64
+//     partial dots of the two lanes, rounded like the oracle). The result
+//     stands when everything left out (groups that left the list, scores
+//     below theta, candidates beyond the buffers) has a key bound strictly
+//     below the take-th selected key.
+//   - A workgroup where any query is unsettled streams every chunk a
+//     second time: each score above the lane's threshold is appended to a
+//     per-lane LDS buffer, folded into a list of the M best when it may
+//     overflow, and the decision runs on those lists.
+//   A query that neither settles (more equal keys at the boundary than the
+//   lists hold, constructed ties, inf / NaN input) is queued; it is never
+//   guessed.
 //
 // * gate_queue_kernel: one wave per queued query, exact scores for every
 //   candidate, lists merged across the wave.
@@ -493,11 +497,11 @@ template <int K>
 __device__ inline void insert_value(float (&l)[K], float x) {
 #pragma unroll
   for (int p = K - 1; p > 0; --p) l[p] = __builtin_amdgcn_fmed3f(l[p - 1], l[p], x);
-  l[0] = fmaxf(l[0], x);
+  l[0] = __builtin_amdgcn_fmed3f(l[0], x, INFINITY);  // max, without canonicalising
 }
 
-template <typename T, int D, int M, int K, int CAP, int WAVES>
-__global__ void __launch_bounds__(WAVES * 64, (D == 64 && M <= 12) ? 3 : 1)
+template <typename T, int D, int M, int K, int CAP, int WAVES, int GB>
+__global__ void __launch_bounds__(WAVES * 64, M <= 12 ? (D == 64 ? 3 : 2) : 1)
 gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                  int32_t* __restrict__ out, const int32_t* __restrict__ cu,
                  int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
@@ -511,8 +515,18 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   constexpr int NT = WAVES * 64;
   constexpr int SR = 64;                           // kbar rows per LDS stage (two chunks)
   constexpr int KCH = (SR * D / 8 + NT - 1) / NT;  // 16-byte chunks per thread per stage
-  __shared__ float s_val[WAVES][CAP][64];
-  __shared__ uint16_t s_id[WAVES][CAP][64];
+  // Per-wave LDS area. Pass 1 keeps there the four scores of each of the
+  // lane's K tracked groups (one float4 per (slot, lane)); the fallback
+  // pass 2 reuses the same bytes for its append buffers (CAP scores and CAP
+  // ids per lane), and the decision for its uncertain ids.
+  static_assert((K & (K - 1)) == 0 && K >= 8, "K is a power of two, at least 8");
+  constexpr int SLOT_BITS = K == 8 ? 3 : (K == 16 ? 4 : 5);
+  static_assert(GB == 4 || GB == 8, "groups of 4 or 8 blocks");
+  constexpr int GPC = 16 / GB;                     // groups per lane and chunk
+  constexpr int REC_BYTES = K * 64 * GB * 4;
+  constexpr int BUF_BYTES = CAP * 64 * 6;
+  constexpr int WAVE_BYTES = REC_BYTES > BUF_BYTES ? REC_BYTES : BUF_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char s_wave[WAVES][WAVE_BYTES];
   __shared__ __attribute__((aligned(16))) uint16_t s_kb[2][SR * KROW];
 
   const int tid = threadIdx.x;
@@ -550,6 +564,15 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     if (live) bq[c] = load_vec16<V>(qrow + 16 * c + 8 * half);
     else bq[c] = V{};
   }
+  // The query half again, from memory: keeps bq out of the registers live
+  // across pass 1 where it is needed only later (rescoring, fallback pass).
+  auto reload_q = [&](V (&dst)[KSTEPS]) {
+    const T* qr = qrow;
+    asm volatile("" : "+v"(qr));
+#pragma unroll
+    for (int c = 0; c < KSTEPS; ++c)
+      dst[c] = live ? load_vec16<V>(qr + 16 * c + 8 * half) : V{};
+  };
   // Error band of this query: E >= |approx - exact| for every candidate.
   float qn = 0.f;
 #pragma unroll
@@ -600,13 +623,14 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     }
   };
 
-  // --- Pass 1: a lower bound on L from every half-chunk's maximum. -------
-  // Each lane keeps the K largest of its per-half-chunk maxima (one score of
-  // one block each, all distinct blocks). The take-th largest of the union of
-  // the two lanes' lists is the take-th best of a subset of the query's
-  // candidates, so it is <= L (the take-th best of all of them); with the
-  // top blocks spread over chunks it is L itself. Every candidate that can
-  // matter then has a key >= R(that value - w) and a score >= theta.
+  // --- Pass 1: every chunk once. Each lane keeps the K largest maxima of
+  // its 4-block groups, and the four scores of each kept group in LDS. The
+  // take-th largest of the union of the two lanes' kept maxima is the
+  // take-th best of a subset of the query's candidates, so it is <= L (the
+  // take-th best of all of them); every candidate that can matter then has
+  // a key >= R(that value - w) and a score >= theta. The kept groups then
+  // hold every such candidate unless the largest group maximum that left
+  // the list reaches theta (then the decision below counts it as a bound).
   // Lane 0 of the wave holds its smallest query, so its own block bounds
   // every lane's: chunks entirely below it need no causal mask.
   const int own_min = __builtin_amdgcn_readfirstlane(own);
@@ -649,34 +673,94 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       step(st + 1, kr0, kr1);
     }
   };
+  // Group keys. A group is four consecutive blocks of one lane (lane half h
+  // holds the groups with (block >> 2) & 1 == h), numbered gid = block >> 3
+  // within the lane. A key is the group's maximum score with its low
+  // mantissa bits replaced by (gid << SLOT_BITS | slot): float order of the
+  // keys is the order of the maxima up to that truncation, and the key
+  // names both the group and the LDS slot holding its four scores.
+  const int max_gid = n_chunks > 0 ? n_chunks * GPC - 1 : 0;
+  const int gid_bits = max_gid > 0 ? 32 - __clz(max_gid) : 0;
+  const uint32_t low_mask = (1u << (SLOT_BITS + gid_bits)) - 1u;
+  // The key's value range: [lo, hi] holds the maximum it was made from.
+  // Keys at or below -3e38 (masked groups, empty slots) mean "none".
+  auto key_lo = [&](float k) {
+    const uint32_t u = __float_as_uint(k);
+    const float f = __uint_as_float((u >> 31) ? (u | low_mask) : (u & ~low_mask));
+    return f <= -3.0e38f ? -INFINITY : f;
+  };
+  auto key_hi = [&](float k) {
+    const uint32_t u = __float_as_uint(k);
+    const float f = __uint_as_float((u >> 31) ? (u & ~low_mask) : (u | low_mask));
+    return f <= -3.0e38f ? -INFINITY : f;
+  };
+  // [K][GB / 4][64] float4: a group's scores in order, four per float4.
+  float4* srec = reinterpret_cast<float4*>(&s_wave[wave][0]) + lane;
+  float gk[K];
+  // Largest key that left the list (or never entered it): every group not
+  // in the list has its maximum <= key_hi(ev).
+  float ev = -INFINITY;
   if (n_chunks > 0) {
-    float tk[K];
+    const float empty = -INFINITY;
 #pragma unroll
-    for (int p = 0; p < K; ++p) tk[p] = -INFINITY;
-    // The maxima of the lane's two 8-block halves of each chunk: where the
-    // best blocks cluster (keys with locality), one maximum per chunk would
-    // leave the bound far below L and pass 2 would collect many more scores.
+    for (int p = 0; p < K; ++p) {
+      gk[p] = __uint_as_float((0xff7fffffu & ~low_mask) | static_cast<uint32_t>(p));
+#pragma unroll
+      for (int h = 0; h < GB / 4; ++h)
+        srec[(p * (GB / 4) + h) * 64] = make_float4(empty, empty, empty, empty);
+    }
+    // Element w of group gid scores block gid 2GB + 8 (w / 4) + 4 half + w % 4.
+    auto track = [&](const float (&x)[GB], int gid) {
+      // Clamped to -FLT_MAX so that replacing low bits keeps it a number.
+      float mx = -3.4028235e38f;
+#pragma unroll
+      for (int w = 0; w < GB; ++w) mx = fmaxf(mx, x[w]);
+      const float old = gk[K - 1];
+      const uint32_t slot = __float_as_uint(old) & (K - 1);
+      const uint32_t low = slot | (static_cast<uint32_t>(gid) << SLOT_BITS);
+      const float key = __uint_as_float((__float_as_uint(mx) & ~low_mask) | low);
+      ev = __builtin_amdgcn_fmed3f(ev, old, key);  // ev <= old always
+      // The key enters the list iff it beats the last entry, whose slot
+      // it takes over.
+      if (key > old) {
+#pragma unroll
+        for (int h = 0; h < GB / 4; ++h)
+          srec[(slot * (GB / 4) + h) * 64] =
+              make_float4(x[4 * h], x[4 * h + 1], x[4 * h + 2], x[4 * h + 3]);
+      }
+      insert_value<K>(gk, key);
+    };
     stream_chunks([&](int ch, const floatx16_t& acc, bool full) {
+      if (full) {
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        float mx = -INFINITY;
-        if (full) {
+        for (int g = 0; g < GPC; ++g) {
+          float x[GB];
 #pragma unroll
-          for (int v = 8 * g; v < 8 * g + 8; ++v) mx = fmaxf(mx, acc[v]);
-        } else {
-#pragma unroll
-          for (int v = 8 * g; v < 8 * g + 8; ++v) {
-            const int b = ch * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-            mx = fmaxf(mx, b < own ? acc[v] : -INFINITY);
-          }
+          for (int w = 0; w < GB; ++w) x[w] = acc[GB * g + w];
+          track(x, ch * GPC + g);
         }
-        insert_value<K>(tk, mx);
+      } else {
+#pragma unroll
+        for (int g = 0; g < GPC; ++g) {
+          const int gid = ch * GPC + g;
+          float x[GB];
+#pragma unroll
+          for (int w = 0; w < GB; ++w)
+            x[w] = gid * 2 * GB + 8 * (w >> 2) + 4 * half + (w & 3) < own ? acc[GB * g + w]
+                                                                         : -INFINITY;
+          track(x, gid);
+        }
       }
     });
-    float pk[K];
+    float lo[K], plo[K];
 #pragma unroll
-    for (int p = 0; p < K; ++p) pk[p] = __shfl_xor(tk[p], 32);
-    const float tau = kth_of_union<K>(tk, pk, take);
+    for (int p = 0; p < K; ++p) {
+      lo[p] = key_lo(gk[p]);
+      plo[p] = __shfl_xor(lo[p], 32);
+    }
+    // The take-th largest of the union of the two lanes' group maxima (each
+    // from a distinct block) is <= L, the take-th best score of the query.
+    const float tau = kth_of_union<K>(lo, plo, take);
     // Keys of the take-th best and above are >= kt0 = R(tau - w); scores
     // below the midpoint between kt0 and the key under it (less a margin
     // of two widths) round below kt0 and cannot be needed.
@@ -689,19 +773,286 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Collection threshold: a > thr0 is a >= theta.
   const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
-  // --- Pass 2: every chunk again. Each score above the lane's threshold
-  // (rare: theta sits about one key below L) is appended, with its
-  // block id, to the lane's LDS buffer; a buffer that may overflow on the
-  // next chunk is folded into the lane's list of its M best scores (value
-  // order; ties are settled by the exact rescoring), and the threshold
-  // rises to the M-th.
+  // Lists of the fallback pass (value order, M best per lane).
   float lv[M];
   int li[M];
+  auto clear_lists = [&]() {
 #pragma unroll
-  for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
-  float* sv = &s_val[wave][0][lane];     // this lane's column of the buffers
-  uint16_t* si = &s_id[wave][0][lane];
-  if (n_chunks > 0) {
+    for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
+  };
+  float rej_mine = -INFINITY;
+
+  float* sv = reinterpret_cast<float*>(&s_wave[wave][0]) + lane;  // [CAP][64]
+  uint16_t* si = reinterpret_cast<uint16_t*>(&s_wave[wave][CAP * 64 * 4]) + lane;
+
+  // --- Merge the two half-lists of this query and decide. -----------------
+  // A query's ranking key is its exact score rounded to float32 and then to
+  // the storage dtype (ties broken by the lower id). Every approximate
+  // score a carries |a - exact| <= E, so its key lies in
+  // [R(a - w), R(a + w)] (R: that rounding, monotone; w: E widened by the
+  // float32 rounding of a -+ E). Keys are coarse (one dtype ulp is far
+  // wider than E), so most intervals are a single key: those candidates
+  // are ranked as they are, and only the ones whose interval straddles a
+  // rounding boundary are rescored exactly. Candidates left out of the
+  // lists score at most U = max(theta, rej) with rej the larger of the two
+  // lanes' rej_mine: their keys are at most R(U + w(U)), and the result
+  // stands when that is below the take-th selected key.
+  constexpr int TS = M <= 12 ? 8 : 16;  // most past blocks one query selects
+  float fv[TS];
+  int fi[TS];
+  uint32_t* su = reinterpret_cast<uint32_t*>(sv);
+  auto decide = [&]() -> bool {
+    const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
+    float pv[M];
+    int pi[M];
+#pragma unroll
+    for (int p = 0; p < M; ++p) {
+      pv[p] = __shfl_xor(lv[p], 32);
+      pi[p] = __shfl_xor(li[p], 32);
+    }
+    // L: the take-th approximate score of the union. At least `take` listed
+    // candidates have keys >= Lk; one whose key interval ends below Lk is
+    // outranked by all of them.
+    const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
+    const float Lk = L > -INFINITY ? Elem<T>::round(L - widen(L)) : -INFINITY;
+    // q or kbar carries inf / NaN, or a score could round to an infinite key.
+    bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
+#pragma unroll
+    for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
+    // The candidates that can still rank in the top `take`, with exact keys,
+    // in (key desc, id asc) order. Both lanes walk the union in the same
+    // order (half 0's list first) and reach identical lists; uncertain ids
+    // wait in the lane's candidate buffer and are rescored (float64) by the
+    // two lanes together, each forming the partial dot over the features it
+    // holds.
+    if (ok && take > 0 && live) {
+      int nu = 0;
+      auto visit = [&](float x, int j) {
+        if (!(x > -INFINITY)) return;
+        const float w = widen(x);
+        const float khi = Elem<T>::round(x + w);
+        if (khi < Lk) return;
+        const float klo = Elem<T>::round(x - w);
+        if (klo == khi) {
+          insert_exact<TS>(fv, fi, klo, j);
+        } else {
+          if (nu < CAP) su[nu * 64] = static_cast<uint32_t>(j);
+          ++nu;
+        }
+      };
+#pragma unroll
+      for (int p = 0; p < M; ++p) visit(half == 0 ? lv[p] : pv[p], half == 0 ? li[p] : pi[p]);
+#pragma unroll
+      for (int p = 0; p < M; ++p) visit(half == 0 ? pv[p] : lv[p], half == 0 ? pi[p] : li[p]);
+      if (nu > CAP) ok = false;  // more straddling candidates than the buffer holds
+      constexpr int R = 2;
+      V qv[KSTEPS];
+      if (nu > 0) reload_q(qv);
+#pragma unroll 1
+      for (int u0 = 0; ok && u0 < nu; u0 += R) {
+        int jr[R];
+        V kv[R][KSTEPS];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          jr[r] = u0 + r < nu ? static_cast<int>(su[(u0 + r) * 64]) : 0;
+          jr[r] = jr[r] < hz ? jr[r] : 0;  // ids come from this lane's lists; a guard
+          const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
+#pragma unroll
+          for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          double part = 0.0;
+#pragma unroll
+          for (int c = 0; c < KSTEPS; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              part += static_cast<double>(static_cast<float>(qv[c][i])) *
+                      static_cast<double>(static_cast<float>(kv[r][c][i]));
+          part += __shfl_xor(part, 32);
+          const float sc = Elem<T>::round(static_cast<float>(part));
+          if (u0 + r < nu && sc > -INFINITY) insert_exact<TS>(fv, fi, sc, jr[r]);
+        }
+      }
+      // Candidates outside the lists must rank below the take-th selected.
+      const float U = fmaxf(rej, theta);
+      if (U > -INFINITY) {
+        const float Uk = Elem<T>::round(U + widen(U));
+        float kt = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
+        if (!(kt > Uk)) ok = false;
+      }
+    }
+    return ok;
+  };
+
+  // --- Decide from the tracked groups. ------------------------------------
+  // Candidates: the scores >= theta of every tracked group whose maximum
+  // may reach theta. Left out: scores below theta, and the groups that
+  // left the list or never entered it (maxima <= key_hi(ev)). Each lane
+  // ranks its own candidates by exact key where the key interval is one
+  // key, the two lanes' lists are merged, and candidates whose interval
+  // straddles a rounding boundary are rescored exactly by both lanes (each
+  // forms the float64 partial dot over its feature half) and inserted by
+  // both, so the pair ends with identical lists.
+  constexpr int NU = 6;  // straddling candidates per lane; more: a bound
+  bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
+#pragma unroll
+  for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
+  // Straddling candidates, the NU with the largest possible keys (sk,
+  // descending) with their ids; sk_over bounds the possible keys of the
+  // ones that did not fit.
+  int sj[NU];
+  float sk[NU];
+  float sk_over = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NU; ++i) { sj[i] = -1; sk[i] = -INFINITY; }
+  // Lower key bounds of every candidate (the exact key where known), the
+  // TS largest, descending.
+  float kl[TS];
+#pragma unroll
+  for (int p = 0; p < TS; ++p) kl[p] = -INFINITY;
+  // The lane's candidates are first compacted into the kbar staging area
+  // (idle after pass 1; every wave is past its last barrier), C per lane,
+  // as (score, id) pairs, plus one entry that takes the writes of
+  // non-candidates once C are held; then only those are ranked.
+  constexpr int CB = (2 * SR * KROW * 2) / (WAVES * 64 * 8) - 1;
+  constexpr int C = CB < 12 ? CB : 12;
+  static_assert(C >= 4, "candidate buffer");
+  float2* cbuf = reinterpret_cast<float2*>(&s_kb[0][0]) + wave * (C + 1) * 64 + lane;
+  int cn = 0;
+  // Largest candidate score that found the buffer full (groups come in
+  // key order, so those are from the lane's lowest-ranked groups): a bound
+  // like key_hi(ev) on what the lists leave out.
+  float drop_max = -INFINITY;
+  if (n_chunks > 0 && live && take > 0) {
+#pragma unroll
+    for (int p = 0; p < K; ++p) {
+      if (key_hi(gk[p]) >= theta) {
+        const uint32_t u = __float_as_uint(gk[p]);
+        const int gid = static_cast<int>((u & low_mask) >> SLOT_BITS);
+#pragma unroll
+        for (int h = 0; h < GB / 4; ++h) {
+          const float4 r4 = srec[((u & (K - 1)) * (GB / 4) + h) * 64];
+          const int b0 = gid * 2 * GB + 8 * h + 4 * half;
+          const float x[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            // Written at the next free entry; only a candidate advances it.
+            cbuf[min(cn, C) * 64] = make_float2(x[w], __int_as_float(b0 + w));
+            drop_max = fmaxf(drop_max, (x[w] > thr0 && cn >= C) ? x[w] : -INFINITY);
+            cn += x[w] > thr0 ? 1 : 0;
+          }
+        }
+      }
+    }
+    const int ce = min(cn, C);
+    for (int e = 0; e < ce; ++e) {
+      const float2 c2 = cbuf[e * 64];
+      const float x = c2.x;
+      const int jx = __float_as_int(c2.y);
+      const float wd = widen(x);
+      const float klo = Elem<T>::round(x - wd);
+      const float khi = Elem<T>::round(x + wd);
+      insert_value<TS>(kl, klo);
+      if (klo == khi) {
+        insert_exact<TS>(fv, fi, klo, jx);
+      } else {
+        float v = khi;
+        int j = jx;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+          const bool gt = v > sk[i];
+          const float nv = gt ? v : sk[i];
+          const int nj = gt ? j : sj[i];
+          v = gt ? sk[i] : v;
+          j = gt ? sj[i] : j;
+          sk[i] = nv;
+          sj[i] = nj;
+        }
+        sk_over = fmaxf(sk_over, v);
+      }
+    }
+    rej_mine = fmaxf(key_hi(ev), drop_max);
+  }
+  {
+    float pv[TS];
+    int pi[TS];
+#pragma unroll
+    for (int p = 0; p < TS; ++p) {
+      pv[p] = __shfl_xor(fv[p], 32);
+      pi[p] = __shfl_xor(fi[p], 32);
+    }
+    merge_top<TS>(fv, fi, pv, pi);
+    // kappa: the take-th largest lower key bound of all candidates of the
+    // query. A straddler whose largest possible key is below kappa ranks
+    // below `take` other candidates: it is left out, and so is what fell
+    // off the straddler list when sk_over is below kappa.
+    float pkl[TS];
+#pragma unroll
+    for (int p = 0; p < TS; ++p) pkl[p] = __shfl_xor(kl[p], 32);
+    const float kappa = take > 0 ? kth_of_union<TS>(kl, pkl, take) : -INFINITY;
+    const float sk_pair = fmaxf(sk_over, __shfl_xor(sk_over, 32));
+    if (sk_pair > -INFINITY && !(sk_pair < kappa)) ok = false;
+    int nk = 0;  // straddlers kept: a prefix of the list
+#pragma unroll
+    for (int i = 0; i < NU; ++i) nk += (sj[i] >= 0 && !(sk[i] < kappa)) ? 1 : 0;
+    const int n_pair = max(nk, __shfl_xor(nk, 32));
+    V qv[KSTEPS];
+    if (ok && n_pair > 0) reload_q(qv);
+#pragma unroll 1
+    for (int u0 = 0; ok && u0 < n_pair; ++u0) {
+      int jm = -1;
+#pragma unroll
+      for (int i = 0; i < NU; ++i) jm = (i == u0 && i < nk) ? sj[i] : jm;
+      const int jp = __shfl_xor(jm, 32);
+      V kv[2][KSTEPS];
+      const int j2[2] = {jm, jp};
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int jr = (j2[r] >= 0 && j2[r] < hz) ? j2[r] : 0;  // a guard
+        const T* krow = kb + static_cast<int64_t>(jr) * D + 8 * half;
+#pragma unroll
+        for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
+      }
+      double part[2] = {0.0, 0.0};
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < KSTEPS; ++c)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            part[r] += static_cast<double>(static_cast<float>(qv[c][i])) *
+                       static_cast<double>(static_cast<float>(kv[r][c][i]));
+      // Mine: my half plus the partner's half of my id (its second part).
+      const double tm = part[0] + __shfl_xor(part[1], 32);
+      const double tp = __shfl_xor(tm, 32);
+      const float sm = Elem<T>::round(static_cast<float>(tm));
+      const float sp = Elem<T>::round(static_cast<float>(tp));
+      if (jm >= 0 && sm > -INFINITY) insert_exact<TS>(fv, fi, sm, jm);
+      if (jp >= 0 && sp > -INFINITY) insert_exact<TS>(fv, fi, sp, jp);
+    }
+    const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
+    const float U = fmaxf(rej, theta);
+    if (ok && take > 0 && live && U > -INFINITY) {
+      const float Uk = Elem<T>::round(U + widen(U));
+      float kt = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
+      if (!(kt > Uk)) ok = false;
+    }
+  }
+
+  // --- Fallback, for the whole workgroup when any query is unsettled: -----
+  // pass 2 streams every chunk again. Each score above the lane's threshold
+  // (rare: theta sits about one key below L) is appended, with its
+  // block id, to the lane's LDS buffer; a buffer that may overflow on the
+  // next chunk is folded into the lane's list of its M best scores, and the
+  // threshold rises to the M-th.
+  if (__syncthreads_or(ok ? 0 : 1) && n_chunks > 0) {
+    reload_q(bq);
+    clear_lists();
     float thr = thr0;
     int cnt = 0;
     auto fold = [&]() {
@@ -763,110 +1114,13 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       if (__any(cnt > CAP - 16)) fold();
     });
     fold();
-  }
-  int n_in_list = 0;
+    int n_in_list = 0;
 #pragma unroll
-  for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
+    for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
+    rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
+    ok = decide();
+  }
 
-  // --- Merge the two half-lists of this query and decide. -----------------
-  // A query's ranking key is its exact score rounded to float32 and then to
-  // the storage dtype (ties broken by the lower id). Every approximate
-  // score a carries |a - exact| <= E, so its key lies in
-  // [R(a - w), R(a + w)] (R: that rounding, monotone; w: E widened by the
-  // float32 rounding of a -+ E). Keys are coarse (one dtype ulp is far
-  // wider than E), so most intervals are a single key: those candidates
-  // are ranked as they are, and only the ones whose interval straddles a
-  // rounding boundary are rescored exactly. Candidates left out of the
-  // lists scored below theta, or at most a lane's M-th entry (rej; none
-  // while the list is not full): their keys are at most R(U + w(U)) with U
-  // the larger of the two, and the result stands when that is below the
-  // take-th selected key.
-  const float rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
-  const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
-  float pv[M];
-  int pi[M];
-#pragma unroll
-  for (int p = 0; p < M; ++p) {
-    pv[p] = __shfl_xor(lv[p], 32);
-    pi[p] = __shfl_xor(li[p], 32);
-  }
-  // L: the take-th approximate score of the union. At least `take` listed
-  // candidates have keys >= Lk; one whose key interval ends below Lk is
-  // outranked by all of them.
-  const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
-  const float Lk = L > -INFINITY ? Elem<T>::round(L - widen(L)) : -INFINITY;
-  // q or kbar carries inf / NaN, or a score could round to an infinite key.
-  bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
-
-  // The candidates that can still rank in the top `take`, with exact keys,
-  // in (key desc, id asc) order. Both lanes walk the union in the same
-  // order (half 0's list first) and reach identical lists; uncertain ids
-  // wait in the lane's candidate buffer and are rescored (float64) by the
-  // two lanes together, each forming the partial dot over the features it
-  // holds.
-  constexpr int TS = M <= 12 ? 8 : 16;  // most past blocks one query selects
-  float fv[TS];
-  int fi[TS];
-#pragma unroll
-  for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
-  uint32_t* su = reinterpret_cast<uint32_t*>(sv);
-  if (ok && take > 0 && live) {
-    int nu = 0;
-    auto visit = [&](float x, int j) {
-      if (!(x > -INFINITY)) return;
-      const float w = widen(x);
-      const float khi = Elem<T>::round(x + w);
-      if (khi < Lk) return;
-      const float klo = Elem<T>::round(x - w);
-      if (klo == khi) {
-        insert_exact<TS>(fv, fi, klo, j);
-      } else {
-        if (nu < CAP) su[nu * 64] = static_cast<uint32_t>(j);
-        ++nu;
-      }
-    };
-#pragma unroll
-    for (int p = 0; p < M; ++p) visit(half == 0 ? lv[p] : pv[p], half == 0 ? li[p] : pi[p]);
-#pragma unroll
-    for (int p = 0; p < M; ++p) visit(half == 0 ? pv[p] : lv[p], half == 0 ? pi[p] : li[p]);
-    if (nu > CAP) ok = false;  // more straddling candidates than the buffer holds
-    constexpr int R = 2;
-#pragma unroll 1
-    for (int u0 = 0; ok && u0 < nu; u0 += R) {
-      int jr[R];
-      V kv[R][KSTEPS];
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        jr[r] = u0 + r < nu ? static_cast<int>(su[(u0 + r) * 64]) : 0;
-        jr[r] = jr[r] < hz ? jr[r] : 0;  // ids come from this lane's buffers; a guard
-        const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
-#pragma unroll
-        for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        double part = 0.0;
-#pragma unroll
-        for (int c = 0; c < KSTEPS; ++c)
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            part += static_cast<double>(static_cast<float>(bq[c][i])) *
-                    static_cast<double>(static_cast<float>(kv[r][c][i]));
-        part += __shfl_xor(part, 32);
-        const float sc = Elem<T>::round(static_cast<float>(part));
-        if (u0 + r < nu && sc > -INFINITY) insert_exact<TS>(fv, fi, sc, jr[r]);
-      }
-    }
-    // Candidates outside the lists must rank below the take-th selected.
-    const float U = fmaxf(rej, theta);
-    if (U > -INFINITY) {
-      const float Uk = Elem<T>::round(U + widen(U));
-      float kt = -INFINITY;
-#pragma unroll
-      for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
-      if (!(kt > Uk)) ok = false;
-    }
-  }
   if (!live || half != 0) return;
   const int64_t qid = hm_query(packed, r, hq, h_q, S, tok, t);
   if (!ok) {
@@ -997,16 +1251,20 @@ template <typename T, int D, int M>
 static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int32_t* cu,
                        const Geometry& g, int take, int cur, const GateWs& ws,
                        hipStream_t st) {
+  // Groups of 4 blocks, 4 waves (3 workgroups per CU at head_dim 64).
+  // Groups of 8 at 8 waves per workgroup (2 per SIMD, the records need
+  // twice the LDS) ran pass 1 no faster and the decision slower.
+  constexpr int GB = 4;
   constexpr int WAVES = 4;
   // Per-lane candidate buffer: one chunk's 16 scores beyond the fold
   // trigger (cnt > CAP - 16); also holds the uncertain ids of the decision.
   constexpr int CAP = M + 8;
-  // Sample list per lane: the take-th best of the union of both lanes'
-  // lists (2K >= take) is the take-th best of some subset of the sample.
-  constexpr int K = M <= 12 ? 5 : 9;
+  // Groups tracked per lane (2K >= take). With 8, a query on i.i.d. keys
+  // finds its candidates outside the kept groups about once in 4e4.
+  constexpr int K = M <= 12 ? 8 : 16;
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq, 32 * WAVES)),
             static_cast<unsigned>(g.rows * g.h_q));
-  hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, K, CAP, WAVES>), grid, dim3(64 * WAVES), 0, st,
+  hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, K, CAP, WAVES, GB>), grid, dim3(64 * WAVES), 0, st,
                      static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
                      g.seq_len, g.h_q, g.h_kv, g.n_blocks, static_cast<int>(g.block_size),
                      take, cur, static_cast<int>(g.slots), ws.kbar_norm, ws.queue,
