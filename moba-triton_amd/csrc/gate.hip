@@ -896,18 +896,9 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // straddles a rounding boundary are rescored exactly by both lanes (each
   // forms the float64 partial dot over its feature half) and inserted by
   // both, so the pair ends with identical lists.
-  constexpr int NU = 6;  // straddling candidates per lane; more: a bound
   bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
 #pragma unroll
   for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
-  // Straddling candidates, the NU with the largest possible keys (sk,
-  // descending) with their ids; sk_over bounds the possible keys of the
-  // ones that did not fit.
-  int sj[NU];
-  float sk[NU];
-  float sk_over = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < NU; ++i) { sj[i] = -1; sk[i] = -INFINITY; }
   // Lower key bounds of every candidate (the exact key where known), the
   // TS largest, descending.
   float kl[TS];
@@ -915,63 +906,72 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   for (int p = 0; p < TS; ++p) kl[p] = -INFINITY;
   // The lane's candidates are first compacted into the kbar staging area
   // (idle after pass 1; every wave is past its last barrier), C per lane,
-  // as (score, id) pairs, plus one entry that takes the writes of
-  // non-candidates once C are held; then only those are ranked.
-  constexpr int CB = (2 * SR * KROW * 2) / (WAVES * 64 * 8) - 1;
-  constexpr int C = CB < 12 ? CB : 12;
+  // plus one entry that takes the writes of non-candidates once C are held;
+  // then only those are ranked. An entry is the score with its low IB bits
+  // replaced by its place among the kept groups' scores (p * GB + w), from
+  // which the block id follows; the decision widens its error band by that
+  // truncation (less than 2^(IB - 23) |score|).
+  constexpr int IB = SLOT_BITS + (GB == 4 ? 2 : 3);
+  constexpr uint32_t IMASK = (1u << IB) - 1u;
+  constexpr int CB = (2 * SR * KROW * 2) / (WAVES * 64 * 4) - 1;
+  constexpr int C = CB < 24 ? CB : 24;
   static_assert(C >= 4, "candidate buffer");
-  float2* cbuf = reinterpret_cast<float2*>(&s_kb[0][0]) + wave * (C + 1) * 64 + lane;
+  float* cbuf = reinterpret_cast<float*>(&s_kb[0][0]) + wave * (C + 1) * 64 + lane;
+  auto widen_c = [&](float a) { return widen(a) + fabsf(a) * ldexpf(1.f, IB - 22); };
   int cn = 0;
   // Largest candidate score that found the buffer full (groups come in
   // key order, so those are from the lane's lowest-ranked groups): a bound
   // like key_hi(ev) on what the lists leave out.
   float drop_max = -INFINITY;
+  int ns = 0;  // straddling candidates held
+  // Candidate e: its (truncated) score, block id and key interval.
+  auto cand = [&](int e, float& x, int& jx, float& klo, float& khi) {
+    x = cbuf[e * 64];
+    const uint32_t ix = __float_as_uint(x) & IMASK;
+    // Block id from the kept group's key: p selects among the registers.
+    uint32_t gu = 0;
+#pragma unroll
+    for (int p = 0; p < K; ++p) gu = static_cast<int>(ix >> 2) / (GB / 4) == p ? __float_as_uint(gk[p]) : gu;
+    const int hh = static_cast<int>(ix >> 2) % (GB / 4);
+    jx = static_cast<int>((gu & low_mask) >> SLOT_BITS) * 2 * GB + 8 * hh + 4 * half +
+         static_cast<int>(ix & 3);
+    const float wd = widen_c(x);
+    klo = Elem<T>::round(x - wd);
+    khi = Elem<T>::round(x + wd);
+  };
   if (n_chunks > 0 && live && take > 0) {
 #pragma unroll
     for (int p = 0; p < K; ++p) {
       if (key_hi(gk[p]) >= theta) {
         const uint32_t u = __float_as_uint(gk[p]);
-        const int gid = static_cast<int>((u & low_mask) >> SLOT_BITS);
 #pragma unroll
         for (int h = 0; h < GB / 4; ++h) {
           const float4 r4 = srec[((u & (K - 1)) * (GB / 4) + h) * 64];
-          const int b0 = gid * 2 * GB + 8 * h + 4 * half;
           const float x[4] = {r4.x, r4.y, r4.z, r4.w};
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             // Written at the next free entry; only a candidate advances it.
-            cbuf[min(cn, C) * 64] = make_float2(x[w], __int_as_float(b0 + w));
+            cbuf[min(cn, C) * 64] = __uint_as_float(
+                (__float_as_uint(x[w]) & ~IMASK) | static_cast<uint32_t>((p * (GB / 4) + h) * 4 + w));
             drop_max = fmaxf(drop_max, (x[w] > thr0 && cn >= C) ? x[w] : -INFINITY);
             cn += x[w] > thr0 ? 1 : 0;
           }
         }
       }
     }
+    // Straddlers move to the front of the buffer (in place: the write
+    // index never passes the read index); ns of them.
     const int ce = min(cn, C);
     for (int e = 0; e < ce; ++e) {
-      const float2 c2 = cbuf[e * 64];
-      const float x = c2.x;
-      const int jx = __float_as_int(c2.y);
-      const float wd = widen(x);
-      const float klo = Elem<T>::round(x - wd);
-      const float khi = Elem<T>::round(x + wd);
+      float x, klo, khi;
+      int jx;
+      cand(e, x, jx, klo, khi);
       insert_value<TS>(kl, klo);
       if (klo == khi) {
         insert_exact<TS>(fv, fi, klo, jx);
       } else {
-        float v = khi;
-        int j = jx;
-#pragma unroll
-        for (int i = 0; i < NU; ++i) {
-          const bool gt = v > sk[i];
-          const float nv = gt ? v : sk[i];
-          const int nj = gt ? j : sj[i];
-          v = gt ? sk[i] : v;
-          j = gt ? sj[i] : j;
-          sk[i] = nv;
-          sj[i] = nj;
-        }
-        sk_over = fmaxf(sk_over, v);
+        cbuf[ns * 64] = x;
+        ++ns;
       }
     }
     rej_mine = fmaxf(key_hi(ev), drop_max);
@@ -986,27 +986,33 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     }
     merge_top<TS>(fv, fi, pv, pi);
     // kappa: the take-th largest lower key bound of all candidates of the
-    // query. A straddler whose largest possible key is below kappa ranks
-    // below `take` other candidates: it is left out, and so is what fell
-    // off the straddler list when sk_over is below kappa.
+    // query. A straddler (key interval over a rounding boundary) whose
+    // largest possible key is below kappa ranks below `take` other
+    // candidates and is left out; the others are rescored. The pair walks
+    // both lanes' straddlers in step; a step where no lane of the wave
+    // holds one that reaches kappa costs no loads.
     float pkl[TS];
 #pragma unroll
     for (int p = 0; p < TS; ++p) pkl[p] = __shfl_xor(kl[p], 32);
     const float kappa = take > 0 ? kth_of_union<TS>(kl, pkl, take) : -INFINITY;
-    const float sk_pair = fmaxf(sk_over, __shfl_xor(sk_over, 32));
-    if (sk_pair > -INFINITY && !(sk_pair < kappa)) ok = false;
-    int nk = 0;  // straddlers kept: a prefix of the list
-#pragma unroll
-    for (int i = 0; i < NU; ++i) nk += (sj[i] >= 0 && !(sk[i] < kappa)) ? 1 : 0;
-    const int n_pair = max(nk, __shfl_xor(nk, 32));
+    const int ns_pair = max(ns, __shfl_xor(ns, 32));
     V qv[KSTEPS];
-    if (ok && n_pair > 0) reload_q(qv);
+    bool q_loaded = false;  // wave-uniform
 #pragma unroll 1
-    for (int u0 = 0; ok && u0 < n_pair; ++u0) {
+    for (int e = 0; ok && e < ns_pair; ++e) {
       int jm = -1;
-#pragma unroll
-      for (int i = 0; i < NU; ++i) jm = (i == u0 && i < nk) ? sj[i] : jm;
+      if (e < ns) {
+        float x, klo, khi;
+        int jx;
+        cand(e, x, jx, klo, khi);
+        if (!(khi < kappa)) jm = jx;
+      }
       const int jp = __shfl_xor(jm, 32);
+      if (!__any(jm >= 0)) continue;
+      if (!q_loaded) {
+        reload_q(qv);
+        q_loaded = true;
+      }
       V kv[2][KSTEPS];
       const int j2[2] = {jm, jp};
 #pragma unroll
