@@ -246,9 +246,16 @@ def other_configs(dev, reps=5):
             moba_attention(qq, kk, vv, cfg, **kw).backward(do)
 
         fb = timed(step, reps, 2)[0]
+        ab = algorithmic_bytes(s, b=b, hq=hq, hkv=hkv, d=d)
+        ab_fwd = sum(ab[x] for x in ("pool", "gate", "csc", "attend", "combine"))
+        ab_all = sum(ab.values())
         row = {"config": name, "shape": [b, s, hq, d], "heads_kv": hkv,
                "fwd_ms": round(fwd, 4), "fwd_bwd_ms": round(fb, 4),
-               "tokens_per_s_fwd_bwd": round(s / (fb * 1e-3), 1)}
+               "tokens_per_s_fwd_bwd": round(s / (fb * 1e-3), 1),
+               # the same traffic model as the headline roofline, at this shape
+               "alg_bytes_fwd": ab_fwd, "alg_bytes_fwd_bwd": ab_all,
+               "hbm_frac_fwd": round(ab_fwd / (fwd * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+               "hbm_frac_fwd_bwd": round(ab_all / (fb * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)}
         if ln is not None:
             row["seq_lens"] = ln
         out.append(row)

@@ -61,7 +61,8 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte chunk
 
-// Workspace layout (bytes): [0, 256) counter; [256, 256 + 4*R*Hkv) norms
+// Workspace layout (bytes): [0, 256) counters (int 0: queued queries, int 1:
+// workgroups that took the fallback stream); [256, 256 + 4*R*Hkv) norms
 // rounded up to 256; then the queue of query ids (int64 each).
 struct GateWs {
   int* counter;
@@ -91,7 +92,7 @@ static GateWs gate_ws(void* base, int64_t rows, int64_t h_kv, int64_t queue_cap)
 __global__ void __launch_bounds__(256)
 gate_init_kernel(unsigned* __restrict__ norm_bits, int64_t n, int* __restrict__ counter) {
   for (int64_t i = threadIdx.x; i < n; i += blockDim.x) norm_bits[i] = 0u;
-  if (threadIdx.x == 0) *counter = 0;
+  if (threadIdx.x < 2) counter[threadIdx.x] = 0;
 }
 
 template <typename T>
@@ -1057,6 +1058,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // next chunk is folded into the lane's list of its M best scores, and the
   // threshold rises to the M-th.
   if (__syncthreads_or(ok ? 0 : 1) && n_chunks > 0) {
+    if (tid == 0) atomicAdd(queue_len + 1, 1);  // fallback workgroups, for tests
     reload_q(bq);
     clear_lists();
     float thr = thr0;

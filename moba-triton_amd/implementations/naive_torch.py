@@ -101,15 +101,17 @@ class NaiveTorchBackend:
         return _attend(q, k, v, sel, cfg.block_size)
 
     def forward_packed(self, q, k, v, cfg: MoBAConfig, cu_seqlens, max_seqlen=None):
-        """[1, T, H, D] packed: every sequence on its own, sequence-local blocks."""
+        """[1, T, H, D] packed: every sequence on its own, sequence-local
+        blocks. Differentiable like `forward_grad` (the pieces are joined with
+        torch.cat, so gradients reach q, k and v of every sequence)."""
         if q.shape[0] != 1:
             raise ValueError(f"packed input must have batch 1, got {q.shape[0]}")
         bounds = [int(x) for x in cu_seqlens.tolist()]
-        out = torch.empty_like(q)
-        for lo, hi in zip(bounds[:-1], bounds[1:]):
-            if hi > lo:
-                out[:, lo:hi] = self.forward(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], cfg)
-        return out
+        pieces = [self.forward_grad(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], cfg)
+                  for lo, hi in zip(bounds[:-1], bounds[1:]) if hi > lo]
+        if not pieces:
+            return torch.empty_like(q)
+        return torch.cat(pieces, dim=1)
 
     def selection(self, q, k, cfg: MoBAConfig) -> torch.Tensor:
         """bool [B, H, S, nb]."""

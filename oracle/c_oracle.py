@@ -38,6 +38,7 @@ def lib():
         _lib.oracle_pool.argtypes = [P, I, I, I, I, I, I, P, I, I, P]
         _lib.oracle_gate.argtypes = [P, P, I, I, I, I, I, I, I, I, I, I, I,
                                      P, I, P]
+        _lib.oracle_gate_strided.argtypes = [P, P] + [I] * 15 + [P]
     return _lib
 
 
@@ -86,6 +87,28 @@ def gate_select(q: torch.Tensor, kbar: torch.Tensor, cfg, cu_seqlens=None,
                       cfg.block_size, take, int(bool(cfg.always_select_current)),
                       slots, _DTYPE_CODE[q.dtype],
                       _ptr(cu) if cu is not None else None, n_seq, _ptr(out))
+    return out
+
+
+def gate_select_strided(q: torch.Tensor, kbar: torch.Tensor, cfg, heads=None,
+                        offset: int = 0, stride: int = 1) -> torch.Tensor:
+    """`gate_select` of a padded batch restricted to query heads `heads`
+    (a range; all by default) and rows offset, offset + stride, ...:
+    ids `[B, len(heads), ceil((S - offset) / stride), slots]` int32."""
+    b, s, hq, d = q.shape
+    hkv, n = kbar.shape[1], kbar.shape[2]
+    heads = range(hq) if heads is None else heads
+    assert heads.step == 1 and 0 <= heads.start < heads.stop <= hq
+    qf = q.detach().cpu().to(torch.float32).contiguous()
+    kf = kbar.detach().cpu().to(torch.float32).contiguous()
+    slots = slots_per_query(cfg)
+    nt = max(0, -(-(s - offset) // stride))
+    out = torch.empty(b, len(heads), nt, slots, dtype=torch.int32)
+    lib().oracle_gate_strided(_ptr(qf), _ptr(kf), b, s, hq, hkv, d, n, cfg.block_size,
+                              past_blocks_selected(cfg, n),
+                              int(bool(cfg.always_select_current)), slots,
+                              _DTYPE_CODE[q.dtype], heads.start, heads.stop, offset, stride,
+                              _ptr(out))
     return out
 
 

@@ -176,4 +176,47 @@ void oracle_gate(const float* q, const float* kbar, int B, int S, int Hq,
     }
 }
 
-int oracle_version(void) { return 1; }
+
+/* The gate of oracle_gate on a subset of a padded batch: query heads
+ * [hq_lo, hq_hi) and the rows t = off, off + stride, ... of every batch row.
+ * Parallel over those query rows, so one head of a 512K-token sequence is
+ * checked in seconds. out: [B, hq_hi - hq_lo, ceil((S - off) / stride),
+ * slots] int32. Same semantics as oracle_gate (src/moba/naive.py:64-146). */
+void oracle_gate_strided(const float* q, const float* kbar, int B, int S,
+                         int Hq, int Hkv, int D, int nb, int bs, int take,
+                         int cur, int slots, int dtype, int hq_lo, int hq_hi,
+                         int off, int stride, int32_t* out) {
+    int g = Hq / Hkv;
+    int nh = hq_hi - hq_lo;
+    long nt = off < S ? (S - off + stride - 1) / stride : 0;
+    long total = (long)B * nh * nt;
+    int nblk = (S + bs - 1) / bs;
+    int budget = take < nblk ? take : nblk;
+#pragma omp parallel
+    {
+        float* val = (float*)malloc(sizeof(float) * (budget + 1));
+        int* idx = (int*)malloc(sizeof(int) * (budget + 2 + slots));
+#pragma omp for schedule(dynamic, 256)
+        for (long i = 0; i < total; ++i) {
+            long ti = i % nt;
+            int h = (int)((i / nt) % nh) + hq_lo;
+            int r = (int)(i / nt / nh);
+            int t = off + (int)ti * stride;
+            const float* kb = kbar + ((size_t)r * Hkv + h / g) * nb * D;
+            const float* qq = q + (((size_t)r * S + t) * Hq + h) * D;
+            int own = t / bs;
+            int cnt = topk_stream(qq, kb, D, own, budget, dtype, val, idx);
+            int m = 0;
+            for (int j = 0; j < cnt; ++j)
+                if (val[j] > -INFINITY) idx[m++] = idx[j];
+            if (cur) idx[m++] = own;
+            qsort(idx, m, sizeof(int), cmp_int);
+            int32_t* o = out + (size_t)i * slots;
+            for (int j = 0; j < slots; ++j) o[j] = j < m ? idx[j] : -1;
+        }
+        free(val);
+        free(idx);
+    }
+}
+
+int oracle_version(void) { return 2; }

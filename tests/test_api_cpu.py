@@ -190,3 +190,23 @@ def test_validation_head_dim_range():
     with pytest.raises(ValueError, match="above 256"):
         z = torch.zeros(1, 256, 2, 512, dtype=torch.bfloat16)
         _validate(z, z, z, cfg)
+
+
+@pytest.mark.parametrize("dtype,d,bs,ok", [
+    (torch.float32, 256, 128, False),   # 256 KiB of keys and values
+    (torch.bfloat16, 256, 256, False),
+    (torch.float32, 256, 64, True),
+    (torch.bfloat16, 256, 128, True),
+    (torch.bfloat16, 128, 128, True),   # MFMA kernel
+])
+def test_validation_rejects_blocks_beyond_lds(dtype, d, bs, ok):
+    """The FMA attend kernel holds a block's keys and values in LDS: a shape
+    that cannot fit is a ValueError before any launch, not a failure inside
+    the library call."""
+    cfg = MoBAConfig(block_size=bs, top_k=2, dtype=dtype)
+    z = torch.zeros(1, 4 * bs, 2, d, dtype=dtype)
+    if ok:
+        _validate(z, z, z, cfg)
+    else:
+        with pytest.raises(ValueError, match="LDS"):
+            _validate(z, z, z, cfg)

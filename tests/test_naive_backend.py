@@ -92,3 +92,18 @@ def test_naive_torch_gradients_match_the_oracle():
     O.moba_attention(*bref, oracle_cfg(cfg), selected=sel).backward(do)
     for x, y in zip(a, bref):
         torch.testing.assert_close(x.grad, y.grad, rtol=1e-9, atol=1e-9)
+
+
+def test_naive_torch_packed_is_differentiable():
+    """Packed gradients equal those of the oracle's packed attention."""
+    cfg = MoBAConfig(block_size=16, top_k=3, dtype=torch.float64)
+    cu = torch.tensor([0, 80, 128, 200], dtype=torch.int32)
+    q, k, v = make_qkv((1, 200, 2, 32), torch.float64, seed=6)
+    do = torch.randn_like(q)
+    a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    get_backend("naive_torch").forward_packed(*a, cfg, cu).backward(do)
+    bref = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    sel = O.moba_selection(q, k, oracle_cfg(cfg), cu_seqlens=cu)
+    O.moba_attention(*bref, oracle_cfg(cfg), selected=sel, cu_seqlens=cu).backward(do)
+    for x, y in zip(a, bref):
+        torch.testing.assert_close(x.grad, y.grad, rtol=1e-9, atol=1e-9)

@@ -205,6 +205,20 @@ def test_c_oracle_equals_torch_oracle(dt):
                        O.mask_to_indices(O.gate_select(q, kb, c), 5))
 
 
+@pytest.mark.parametrize("heads,off,stride", [(range(0, 4), 0, 1), (range(1, 3), 3, 8),
+                                              (range(3, 4), 5, 7)])
+def test_strided_c_gate_equals_the_torch_gate_restricted(heads, off, stride):
+    """The C oracle's head / row subset (used on whole heads at 512K) is the
+    torch oracle's full gate read at those heads and rows, for two batch
+    rows, GQA and a ragged tail."""
+    c = cfg(64, 6)
+    q, k, _ = (t.to(torch.bfloat16) for t in qkv(2, 1000, 4, 64, dtype=torch.float32, seed=12))
+    kbar = O.pool_blocks(k[:, :, :2].contiguous(), 64)
+    full = O.mask_to_indices(O.gate_select(q, kbar, c), 6)
+    got = c_oracle.gate_select_strided(q, kbar, c, heads=heads, offset=off, stride=stride)
+    assert torch.equal(got, full[:, heads.start:heads.stop, off::stride])
+
+
 @pytest.mark.parametrize("s,bs,tk", [(2048, 64, 5), (1000, 32, 8)])
 def test_gate_rows_equal_the_full_gate_restricted(s, bs, tk):
     """The row-subset gate (used at full sequence lengths) is the full gate

@@ -84,3 +84,36 @@ def test_noalloc_rejects_oversized(device):
                                64, 4099, 128, 8, 7, 1, 0, None)
     assert rc == _lib.MOBA_ERR_WORKSPACE
     assert b"static scratch limit" in lib.moba_last_error()
+
+
+def test_noalloc_replays_in_a_graph_match_the_oracle(device):
+    """The callers this entry point is for capture it: one eager call first
+    (it takes the scratch address on the device), then a capture of
+    moba_gate_noalloc alone, replayed on new q / kbar copied into the
+    captured buffers, with eager work in between; every replay's ids equal
+    the C oracle's."""
+    from oracle import c_oracle
+    from conftest import oracle_cfg
+
+    cfg = MoBAConfig(block_size=64, top_k=8, dtype=torch.bfloat16)
+    shape = (1, 4096, 2, 64)
+    q0, k0, _ = make_qkv(shape, torch.bfloat16, seed=40, device=device)
+    qs, kbs = q0.clone(), pool_blocks(k0, cfg)
+    out = torch.full((1, 2, shape[1], cfg.slots()), -9, device=device, dtype=torch.int32)
+    args = _gate_args(qs, kbs, cfg, out)
+    _lib.call("moba_gate_noalloc", *args, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.call("moba_gate_noalloc", *args, _lib.stream_handle(device))
+    for seed in (41, 42, 43):
+        q, k, _ = make_qkv(shape, torch.bfloat16, seed=seed, device=device)
+        kb = pool_blocks(k, cfg)
+        qs.copy_(q)
+        kbs.copy_(kb)
+        out.fill_(-9)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = c_oracle.gate_select(q.cpu(), kb.cpu(), oracle_cfg(cfg))
+        bad = (out.cpu() != want).any(-1)
+        assert not bool(bad.any()), f"replay {seed}: {int(bad.sum())} queries differ"
