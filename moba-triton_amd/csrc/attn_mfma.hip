@@ -459,7 +459,14 @@ bwd_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float s_lse_[ST][NQ];
   __shared__ __attribute__((aligned(16))) float s_delta_[ST][NQ];
   __shared__ __attribute__((aligned(16))) int s_lim_[ST][NQ];
-  __shared__ int64_t s_dst_[ST][NQ];
+  // dQ destinations by step parity: the stores of step g read them after the
+  // dS barrier, while step g + 1's are already being staged.
+  __shared__ int64_t s_dst_[ST][2][NQ];
+  // dQ tiles per wave ([q][d], 32 x 32, row stride DQS) on their way out as
+  // 16-byte chunks; private to the wave, so only a wave barrier orders them.
+  constexpr int TPW = DT * (NQ / 32) / (BS / 32);
+  constexpr int DQS = 40;
+  __shared__ __attribute__((aligned(16))) uint16_t DQs_[sizeof(A) == 2 ? ST * (BS / 32) * TPW * 32 * DQS : 8];
   static_assert((NQ * RS * 2) % 16 == 0 && (kRows * 2) % 16 == 0, "16-byte aligned carving");
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
@@ -487,7 +494,6 @@ bwd_mfma_kernel(AttnArgs a) {
   float* s_lse = s_lse_[stream];
   float* s_delta = s_delta_[stream];
   int* s_lim = s_lim_[stream];
-  int64_t* s_dst = s_dst_[stream];
   const int h = lane >> 5;
   const int col = lane & 31;
   const int mykey = wave * 32 + col;  // the key this lane holds in S / dP / dV / dK
@@ -600,24 +606,16 @@ bwd_mfma_kernel(AttnArgs a) {
     c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
     derive();  // s_qoff now describes step 1; every thread read step 0's above
   }
-  // vmcnt(0): the K / V operands and the prologue loads are all resident, so
-  // the loop's wait counts start from an empty queue on every path.
-  __builtin_amdgcn_s_waitcnt(0x0f70);
-
-  // Every stream runs the same number of iterations (the barriers are
-  // shared); a stream past the column's end runs a dead step: zero rows,
-  // every entry hidden, nothing stored.
-  for (int32_t base = 0; base < c.n; base += ST * NQ) {
-    const int32_t g0 = base + stream * NQ;
-    const bool act = g0 < c.n;
-    __syncthreads();  // previous step fully consumed; s_qoff of step g + 1 visible
+  // Stages one step: its limits, row statistics, dQ destinations (parity
+  // par) and its Q / dO rows, row-major (the dV / dK products read them
+  // transposed). A dead step (act false) gets zero rows and no entries.
+  auto stage = [&](bool act, int par) {
     if (stid < NQ) {
       s_lim[stid] = act ? c_lim : -1;
       s_lse[stid] = c_lse;
       s_delta[stid] = c_dl;
-      s_dst[stid] = act ? c_dst : -1;
+      s_dst_[stream][par][stid] = act ? c_dst : -1;
     }
-    // Q and dO rows, row-major; the dV / dK products read them transposed.
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = stid + u * NT;
@@ -626,7 +624,24 @@ bwd_mfma_kernel(AttnArgs a) {
       *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = pv[u] && act ? pq[u] : u32x4{0, 0, 0, 0};
       *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = pv[u] && act ? po[u] : u32x4{0, 0, 0, 0};
     }
+  };
+  // vmcnt(0): the K / V operands and the prologue loads are all resident, so
+  // the loop's wait counts start from an empty queue on every path.
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+  if (c.n > 0) stage(stream * NQ < c.n, 0);
+
+  // Every stream runs the same number of iterations (the barriers are
+  // shared); a stream past the column's end runs a dead step: zero rows,
+  // every entry hidden, nothing stored. Two workgroup barriers per step:
+  // the first makes the step's staging visible (and orders the previous
+  // step's dQ reads of dS^T before this step's dS writes), the second makes
+  // dS visible and frees Qs / Os, which the next step is then staged into
+  // while this step's dQ is formed.
+  int par = 0;
+  for (int32_t base = 0; base < c.n; base += ST * NQ, par ^= 1) {
+    const int32_t g0 = base + stream * NQ;
     __syncthreads();
+    const int64_t* s_dst = s_dst_[stream][par];
     // Every entry of the step sees the whole block (a strictly past, full
     // block) or is dead: the causal masks can go. A dead entry's Q and dO
     // rows are zero, so it adds nothing to dK / dV either way, and its dQ is
@@ -713,7 +728,6 @@ bwd_mfma_kernel(AttnArgs a) {
 
     // dQ^T[d][q] over all BS keys; (feature tile, query tile) pairs spread
     // over the waves.
-    constexpr int TPW = DT * QT / NW;
     static_assert(DT * QT % NW == 0, "dQ tiles must spread evenly over the waves");
     // B operand (dS^T, keys 16j + 8h + [0, 8) of query 32qt + col) read
     // transposed from the [key][q] rows: lane (g, r) addresses key
@@ -747,55 +761,61 @@ bwd_mfma_kernel(AttnArgs a) {
       }
     }
     // dq[t][v] is feature 32dt + 8(v/4) + 4h + v%4 of query 32qt + col.
+    const bool next = base + ST * NQ < c.n;  // uniform: the loop runs again
     if constexpr (sizeof(A) == 2) {
-      // dQ through LDS (Qs): each wave its 32 x 32 tiles, 16-byte chunks out.
+      // dQ through this wave's LDS tiles, read back as 16-byte chunks.
+      uint16_t* dqs = DQs_ + ((stream * NW + wave) * TPW) * 32 * DQS;
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int tt = wave + t * NW;
-        const int dt = tt % DT, qt = tt / DT;
+      for (int t = 0; t < TPW; ++t)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4)
-          store4<A>(reinterpret_cast<A*>(&Qs[(qt * 32 + col) * RS + dt * 32 + 8 * q4 + 4 * h]),
+          store4<A>(reinterpret_cast<A*>(&dqs[(t * 32 + col) * DQS + 8 * q4 + 4 * h]),
                     dq[t][4 * q4] * a.scale, dq[t][4 * q4 + 1] * a.scale,
                     dq[t][4 * q4 + 2] * a.scale, dq[t][4 * q4 + 3] * a.scale);
-      }
-      // Each wave reads back only the 32 x 32 tiles it wrote (four 16-byte
-      // chunks per query and tile), so a wave-level barrier orders them; the
-      // next step's staging waits at the loop's first barrier. s_qoff, which
-      // derive() rewrites, was last read before the dS barrier.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (more) {
-        c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
-        derive();  // waits for every load in flight, before the stores
-      }
+      u32x4 val[TPW][2];
+      int64_t dst[TPW][2];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
-        const int tt = wave + t * NW;
-        const int dt = tt % DT, qt = tt / DT;
+        const int qt = (wave + t * NW) / DT;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int ci = lane + 64 * u;
-          const int q = qt * 32 + (ci >> 2);
-          const int d8 = dt * 32 + (ci & 3) * 8;
-          const int64_t dst = s_dst[q];
-          const u32x4 val = *reinterpret_cast<const u32x4*>(&Qs[q * RS + d8]);
-          if (dst >= 0) *reinterpret_cast<u32x4*>(dq_out + dst * D + d8) = val;
+          val[t][u] = *reinterpret_cast<const u32x4*>(&dqs[(t * 32 + (ci >> 2)) * DQS + (ci & 3) * 8]);
+          dst[t][u] = s_dst[qt * 32 + (ci >> 2)];
+        }
+      }
+      if (more) {
+        c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
+        derive();  // waits for every load in flight
+      }
+      if (next) stage(more, par ^ 1);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int dt = (wave + t * NW) % DT;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int d8 = dt * 32 + ((lane + 64 * u) & 3) * 8;
+          if (dst[t][u] >= 0) *reinterpret_cast<u32x4*>(dq_out + dst[t][u] * D + d8) = val[t][u];
         }
       }
     } else {
+      int64_t dst[TPW];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) dst[t] = s_dst[((wave + t * NW) / DT) * 32 + col];
       if (more) {
         c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
         derive();
       }
+      if (next) stage(more, par ^ 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int tt = wave + t * NW;
-        const int dt = tt % DT, qt = tt / DT;
-        const int64_t dst = s_dst[qt * 32 + col];
-        if (dst >= 0) {
-          A* base = dq_out + dst * D + dt * 32 + 4 * h;
+        const int dt = tt % DT;
+        if (dst[t] >= 0) {
+          A* base = dq_out + dst[t] * D + dt * 32 + 4 * h;
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4)
             store4<A>(base + 8 * q4, dq[t][4 * q4] * a.scale, dq[t][4 * q4 + 1] * a.scale,

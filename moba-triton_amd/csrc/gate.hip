@@ -36,13 +36,24 @@
 //     stands when everything left out (groups that left the list, scores
 //     below theta, candidates beyond the buffers) has a key bound strictly
 //     below the take-th selected key.
-//   - A workgroup where any query is unsettled streams every chunk a
-//     second time: each score above the lane's threshold is appended to a
-//     per-lane LDS buffer, folded into a list of the M best when it may
-//     overflow, and the decision runs on those lists.
-//   A query that neither settles (more equal keys at the boundary than the
-//   lists hold, constructed ties, inf / NaN input) is queued; it is never
-//   guessed.
+//   - A workgroup with a few unsettled queries (at most 4) streams every
+//     chunk a second time: each score above the lane's threshold is
+//     appended to a per-lane LDS buffer, folded into a list of the M best
+//     when it may overflow, and the decision runs on those lists. A
+//     workgroup with more hands them, with their theta, to lists per
+//     (row, query head, position bucket).
+//
+// * gate_fallback_kernel: tiles of 128 such queries stream every chunk up
+//   to the tile's horizon, as the second stream above, but the lists rank
+//   by (largest key the score can have, id): everything a full list left
+//   out ranks below its last entry, so many equal keys at the boundary
+//   (keys sharing a large common component) settle by id, as the oracle
+//   breaks ties, instead of going to the queue. The work follows the
+//   number of unsettled queries, not the number of workgroups holding one.
+//
+//   A query that settles nowhere (more straddling candidates than the
+//   buffers hold, constructed ties, inf / NaN input) is queued; it is
+//   never guessed.
 //
 // * gate_queue_kernel: one wave per queued query, exact scores for every
 //   candidate, lists merged across the wave.
@@ -61,25 +72,52 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte chunk
 
-// Workspace layout (bytes): [0, 256) counters (int 0: queued queries, int 1:
-// workgroups that took the fallback stream); [256, 256 + 4*R*Hkv) norms
-// rounded up to 256; then the queue of query ids (int64 each).
+// Unsettled queries of gate_mfma_kernel wait for gate_fallback_kernel in
+// lists per (row, query head, position bucket): (t, theta bits) pairs, cap
+// entries per list (a bucket holds cap consecutive positions).
+constexpr int kFbBuckets = 16;
+struct FbLists {
+  int2* list;
+  int* count;
+  int64_t cap;
+};
+
+// Workspace layout (bytes), each part starting on a 256-byte boundary:
+// counters (int 0: queued queries, int 1: tiles the fallback kernel ran);
+// max |kbar| per (row, kv head); the queue of query ids (int64 each, one per
+// query); the fallback list lengths (int per (row, query head, bucket));
+// the fallback lists ((t, theta) int2 entries, a bucket's positions each).
 struct GateWs {
   int* counter;
   float* kbar_norm;
   int64_t* queue;
-  int64_t queue_cap;
+  int* fb_count;
+  int2* fb_list;
+  int64_t fb_cap;  // entries per fallback list
+  size_t bytes;    // total size of the layout
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static GateWs gate_ws(void* base, int64_t rows, int64_t h_kv, int64_t queue_cap) {
+// norms: (row, kv head) pairs; pairs: (row, query head) pairs.
+static GateWs gate_ws(void* base, int64_t norms, int64_t pairs, int64_t rows_per_seq) {
+  // A null base only sizes the layout.
   char* p = static_cast<char*>(base);
+  auto at = [&](size_t off) { return p ? p + off : nullptr; };
   GateWs w;
+  const int64_t fb_cap = (rows_per_seq + kFbBuckets - 1) / kFbBuckets;
+  size_t o = 256;
   w.counter = reinterpret_cast<int*>(p);
-  w.kbar_norm = reinterpret_cast<float*>(p + 256);
-  w.queue = reinterpret_cast<int64_t*>(p + 256 + align256(sizeof(float) * rows * h_kv));
-  w.queue_cap = queue_cap;
+  w.kbar_norm = reinterpret_cast<float*>(at(o));
+  o += align256(sizeof(float) * norms);
+  w.queue = reinterpret_cast<int64_t*>(at(o));
+  o += align256(sizeof(int64_t) * pairs * rows_per_seq);
+  w.fb_count = reinterpret_cast<int*>(at(o));
+  o += align256(sizeof(int) * pairs * kFbBuckets);
+  w.fb_list = reinterpret_cast<int2*>(at(o));
+  o += sizeof(int2) * pairs * kFbBuckets * fb_cap;
+  w.fb_cap = fb_cap;
+  w.bytes = o;
   return w;
 }
 
@@ -90,8 +128,10 @@ static GateWs gate_ws(void* base, int64_t rows, int64_t h_kv, int64_t queue_cap)
 // gives each block of kbar a thread and folds the maxima in with atomicMax.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
-gate_init_kernel(unsigned* __restrict__ norm_bits, int64_t n, int* __restrict__ counter) {
+gate_init_kernel(unsigned* __restrict__ norm_bits, int64_t n, int* __restrict__ counter,
+                 int* __restrict__ fb_count, int64_t n_fb) {
   for (int64_t i = threadIdx.x; i < n; i += blockDim.x) norm_bits[i] = 0u;
+  for (int64_t i = threadIdx.x; i < n_fb; i += blockDim.x) fb_count[i] = 0;
   if (threadIdx.x < 2) counter[threadIdx.x] = 0;
 }
 
@@ -486,6 +526,27 @@ template <> __device__ inline float key_below<f16_t>(float v) {
   return f16_to_float(v > 0.f ? b - 1 : (v < 0.f ? b + 1 : 0x8001));
 }
 
+// Inserts (x, j) with the largest key k it can have into a list sorted by
+// (key desc, id asc); the last entry falls off. The entry shifted down at
+// each step is compared under the same order (ids break equal keys).
+template <int M>
+__device__ inline void insert_keyed(float (&key)[M], float (&val)[M], int (&idx)[M], float k,
+                                    float x, int j) {
+#pragma unroll
+  for (int p = 0; p < M; ++p) {
+    const bool gt = k > key[p] || (k == key[p] && j < idx[p]);
+    const float nk = gt ? k : key[p];
+    const float nv = gt ? x : val[p];
+    const int ni = gt ? j : idx[p];
+    k = gt ? key[p] : k;
+    x = gt ? val[p] : x;
+    j = gt ? idx[p] : j;
+    key[p] = nk;
+    val[p] = nv;
+    idx[p] = ni;
+  }
+}
+
 template <typename V>
 __device__ inline V load_vec16(const void* p) {
   uint4 u = *reinterpret_cast<const uint4*>(p);
@@ -501,14 +562,16 @@ __device__ inline void insert_value(float (&l)[K], float x) {
   l[0] = __builtin_amdgcn_fmed3f(l[0], x, INFINITY);  // max, without canonicalising
 }
 
-template <typename T, int D, int M, int K, int CAP, int WAVES, int GB>
-__global__ void __launch_bounds__(WAVES * 64, M <= 12 ? (D == 64 ? 3 : 2) : 1)
-gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
-                 int32_t* __restrict__ out, const int32_t* __restrict__ cu,
-                 int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
-                 int take, int cur, int slots, const float* __restrict__ kbar_norm,
-                 int64_t* __restrict__ queue, int* __restrict__ queue_len,
-                 int64_t rows_per_seq) {
+// One tile of 32 * WAVES queries of one (row, query head): the queries
+// t0 .. t0 + 32 WAVES - 1 (first kernel, FB false), or entries e0 .. of a
+// fallback list (FB true; `ent` is the list, n_ent its length).
+template <typename T, int D, int M, int K, int CAP, int WAVES, int GB, bool FB>
+__device__ __forceinline__ void gate_tile(
+    const T* __restrict__ q, const T* __restrict__ kbar, int32_t* __restrict__ out,
+    const int32_t* __restrict__ cu, int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks,
+    int bs, int take, int cur, int slots, const float* __restrict__ kbar_norm,
+    int64_t* __restrict__ queue, int* __restrict__ queue_len, int64_t rows_per_seq,
+    int64_t rh, int64_t first, const FbLists& fb, const int2* __restrict__ ent, int n_ent) {
   using Ops = MfmaOps<T>;
   using V = typename Ops::vec;
   constexpr int KSTEPS = D / 16;
@@ -537,22 +600,41 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   const int col = lane & 31;
   const bool packed = cu != nullptr;
 
-  const int64_t rh = blockIdx.y;
   const int64_t r = rh / h_q;
   const int64_t hq = rh % h_q;
   const int64_t hk = hq / (h_q / h_kv);
   const SeqSpan sp = seq_span(cu, r, S);
-  // Tiles are numbered from the end so the longest ones start first.
-  const int64_t n_tiles = (rows_per_seq + 32 * WAVES - 1) / (32 * WAVES);
-  const int64_t tile = n_tiles - 1 - blockIdx.x;
-  const int64_t twg = tile * 32 * WAVES;
-  if (twg >= sp.len) return;  // uniform over the workgroup
-  const int64_t t = twg + wave * 32 + col;
-  const bool live = t < sp.len;
-  const int own = live ? static_cast<int>(t / bs) : 0;
-  // Blocks any query of the workgroup may rank: [0, hz).
-  const int64_t last_wg = (twg + 32 * WAVES - 1 < sp.len ? twg + 32 * WAVES - 1 : sp.len - 1);
-  const int hz = static_cast<int>(last_wg / bs);
+  int64_t t;
+  bool live;
+  int own;
+  int hz;  // blocks any query of the workgroup may rank: [0, hz)
+  float theta_in = -INFINITY;
+  if constexpr (!FB) {
+    if (first >= sp.len) return;  // uniform over the workgroup
+    t = first + wave * 32 + col;
+    live = t < sp.len;
+    own = live ? static_cast<int>(t / bs) : 0;
+    const int64_t last_wg = (first + 32 * WAVES - 1 < sp.len ? first + 32 * WAVES - 1 : sp.len - 1);
+    hz = static_cast<int>(last_wg / bs);
+  } else {
+    // Queries of one list in no particular order: the horizon is the
+    // largest own block of the tile.
+    __shared__ int s_hz;
+    const int64_t e = first + wave * 32 + col;
+    live = e < n_ent;
+    const int2 en = live ? ent[e] : make_int2(0, 0);
+    t = en.x;
+    theta_in = __int_as_float(en.y);
+    own = live ? static_cast<int>(t / bs) : 0;
+    int m = own;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, __shfl_xor(m, off));
+    if (tid == 0) s_hz = 0;
+    __syncthreads();
+    if (lane == 0) atomicMax(&s_hz, m);
+    __syncthreads();
+    hz = s_hz;
+  }
   const T* kb = kbar + (r * h_kv + hk) * n_blocks * D;
   const int64_t tok = sp.bos + (live ? t : 0);
   const T* qrow = q + (tok * h_q + hq) * D;
@@ -634,8 +716,16 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // the list reaches theta (then the decision below counts it as a bound).
   // Lane 0 of the wave holds its smallest query, so its own block bounds
   // every lane's: chunks entirely below it need no causal mask.
-  const int own_min = __builtin_amdgcn_readfirstlane(own);
-  float theta = -INFINITY;
+  int own_min;
+  if constexpr (!FB) {
+    own_min = __builtin_amdgcn_readfirstlane(own);
+  } else {
+    int m = live ? own : 0x7fffffff;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
+    own_min = m;
+  }
+  float theta = theta_in;
   auto stream_chunks = [&](auto&& body) {
     // step(st): score both chunks of stage st (two independent MFMA chains
     // over one A-operand buffer), move stage st + 1 from `next` into LDS,
@@ -701,7 +791,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Largest key that left the list (or never entered it): every group not
   // in the list has its maximum <= key_hi(ev).
   float ev = -INFINITY;
-  if (n_chunks > 0) {
+  if (!FB && n_chunks > 0) {
     const float empty = -INFINITY;
 #pragma unroll
     for (int p = 0; p < K; ++p) {
@@ -774,12 +864,17 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // Collection threshold: a > thr0 is a >= theta.
   const float thr0 = theta > -INFINITY ? nextafterf(theta, -INFINITY) : -INFINITY;
 
-  // Lists of the fallback pass (value order, M best per lane).
-  float lv[M];
+  // Lists of the fallback pass: the lane's M best candidates by (largest
+  // key the score can have, id asc), approximate scores beside them.
+  float lk[FB ? M : 1], lv[M];
   int li[M];
   auto clear_lists = [&]() {
 #pragma unroll
     for (int p = 0; p < M; ++p) { lv[p] = -INFINITY; li[p] = 0x7fffffff; }
+    if constexpr (FB) {
+#pragma unroll
+      for (int p = 0; p < M; ++p) lk[p] = -INFINITY;
+    }
   };
   float rej_mine = -INFINITY;
 
@@ -794,15 +889,19 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
   // float32 rounding of a -+ E). Keys are coarse (one dtype ulp is far
   // wider than E), so most intervals are a single key: those candidates
   // are ranked as they are, and only the ones whose interval straddles a
-  // rounding boundary are rescored exactly. Candidates left out of the
-  // lists score at most U = max(theta, rej) with rej the larger of the two
-  // lanes' rej_mine: their keys are at most R(U + w(U)), and the result
-  // stands when that is below the take-th selected key.
+  // rounding boundary are rescored exactly. Scores below theta have keys
+  // below every selected key; what a full list left out ranks below its
+  // last entry, so the result stands when each lane's last entry ranks at
+  // or below the take-th selected (equal keys: ids asc). Many equal keys
+  // at the boundary thus settle by id, as the oracle breaks the tie.
   constexpr int TS = M <= 12 ? 8 : 16;  // most past blocks one query selects
   float fv[TS];
   int fi[TS];
   uint32_t* su = reinterpret_cast<uint32_t*>(sv);
-  auto decide = [&]() -> bool {
+  // The first kernel's own fallback ranks its lists by approximate score
+  // alone: what they left out scores at most rej, the larger of the two
+  // lanes' rej_mine, and its key is at most R(U + w(U)), U = max(theta, rej).
+  auto decide_value = [&]() -> bool {
     const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
     float pv[M];
     int pi[M];
@@ -887,6 +986,113 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     }
     return ok;
   };
+  // The fallback kernel's lists rank by (largest key, id), so equal keys at
+  // the boundary settle by id.
+  auto decide_keyed = [&]() -> bool {
+    // Everything a lane's full list left out ranks below its last entry
+    // (key rk, id rid) in (key desc, id asc) order: an entry that fell off
+    // ranked below the entry then last, and a score that was never
+    // appended could not reach a key above rk, with an id past the list's.
+    const bool full = lk[M - 1] > -INFINITY;
+    const float rk_m = full ? lk[M - 1] : -INFINITY;
+    const int rid_m = full ? li[M - 1] : 0x7fffffff;
+    const float rk_p = __shfl_xor(rk_m, 32);
+    const int rid_p = __shfl_xor(rid_m, 32);
+    float pk[M], pv[M];
+    int pi[M];
+#pragma unroll
+    for (int p = 0; p < M; ++p) {
+      pk[p] = __shfl_xor(lk[p], 32);
+      pv[p] = __shfl_xor(lv[p], 32);
+      pi[p] = __shfl_xor(li[p], 32);
+    }
+    // q or kbar carries inf / NaN, or a score could round to an infinite key.
+    bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
+#pragma unroll
+    for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
+    if (ok && take > 0 && live) {
+      // Lk: the take-th largest lower key bound of the union; a candidate
+      // whose largest key is below it ranks below `take` others.
+      float kl[TS];
+#pragma unroll
+      for (int p = 0; p < TS; ++p) kl[p] = -INFINITY;
+      auto lower = [&](float x) { return x > -INFINITY ? Elem<T>::round(x - widen(x)) : -INFINITY; };
+#pragma unroll
+      for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? lv[p] : pv[p]));
+#pragma unroll
+      for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? pv[p] : lv[p]));
+      float Lk = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < TS; ++p) Lk = p == take - 1 ? kl[p] : Lk;
+      // The candidates that can still rank in the top `take`, with exact keys,
+      // in (key desc, id asc) order. Both lanes walk the union in the same
+      // order (half 0's list first) and reach identical lists; uncertain ids
+      // wait in the lane's candidate buffer and are rescored (float64) by the
+      // two lanes together, each forming the partial dot over the features it
+      // holds.
+      int nu = 0;
+      auto visit = [&](float x, int j) {
+        if (!(x > -INFINITY)) return;
+        const float w = widen(x);
+        const float khi = Elem<T>::round(x + w);
+        if (khi < Lk) return;
+        const float klo = Elem<T>::round(x - w);
+        if (klo == khi) {
+          insert_exact<TS>(fv, fi, klo, j);
+        } else {
+          if (nu < CAP) su[nu * 64] = static_cast<uint32_t>(j);
+          ++nu;
+        }
+      };
+#pragma unroll
+      for (int p = 0; p < M; ++p) visit(half == 0 ? lv[p] : pv[p], half == 0 ? li[p] : pi[p]);
+#pragma unroll
+      for (int p = 0; p < M; ++p) visit(half == 0 ? pv[p] : lv[p], half == 0 ? pi[p] : li[p]);
+      if (nu > CAP) ok = false;  // more straddling candidates than the buffer holds
+      constexpr int R = 2;
+      V qv[KSTEPS];
+      if (nu > 0) reload_q(qv);
+#pragma unroll 1
+      for (int u0 = 0; ok && u0 < nu; u0 += R) {
+        int jr[R];
+        V kv[R][KSTEPS];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          jr[r] = u0 + r < nu ? static_cast<int>(su[(u0 + r) * 64]) : 0;
+          jr[r] = jr[r] < hz ? jr[r] : 0;  // ids come from this lane's lists; a guard
+          const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
+#pragma unroll
+          for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          double part = 0.0;
+#pragma unroll
+          for (int c = 0; c < KSTEPS; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              part += static_cast<double>(static_cast<float>(qv[c][i])) *
+                      static_cast<double>(static_cast<float>(kv[r][c][i]));
+          part += __shfl_xor(part, 32);
+          const float sc = Elem<T>::round(static_cast<float>(part));
+          if (u0 + r < nu && sc > -INFINITY) insert_exact<TS>(fv, fi, sc, jr[r]);
+        }
+      }
+      float kt = -INFINITY;
+      int it = 0x7fffffff;
+#pragma unroll
+      for (int p = 0; p < TS; ++p) {
+        kt = p == take - 1 ? fv[p] : kt;
+        it = p == take - 1 ? fi[p] : it;
+      }
+      // Scores below theta have keys below every selected key.
+      if (theta > -INFINITY && !(kt > Elem<T>::round(theta + widen(theta)))) ok = false;
+      // What the lists left out must rank below the take-th selected.
+      if (rk_m > kt || (rk_m == kt && rid_m < it)) ok = false;
+      if (rk_p > kt || (rk_p == kt && rid_p < it)) ok = false;
+    }
+    return ok;
+  };
 
   // --- Decide from the tracked groups. ------------------------------------
   // Candidates: the scores >= theta of every tracked group whose maximum
@@ -940,7 +1146,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     klo = Elem<T>::round(x - wd);
     khi = Elem<T>::round(x + wd);
   };
-  if (n_chunks > 0 && live && take > 0) {
+  if (!FB && n_chunks > 0 && live && take > 0) {
 #pragma unroll
     for (int p = 0; p < K; ++p) {
       if (key_hi(gk[p]) >= theta) {
@@ -977,7 +1183,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     }
     rej_mine = fmaxf(key_hi(ev), drop_max);
   }
-  {
+  if constexpr (!FB) {
     float pv[TS];
     int pi[TS];
 #pragma unroll
@@ -1051,21 +1257,38 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     }
   }
 
-  // --- Fallback, for the whole workgroup when any query is unsettled: -----
-  // pass 2 streams every chunk again. Each score above the lane's threshold
-  // (rare: theta sits about one key below L) is appended, with its
-  // block id, to the lane's LDS buffer; a buffer that may overflow on the
-  // next chunk is folded into the lane's list of its M best scores, and the
-  // threshold rises to the M-th.
-  if (__syncthreads_or(ok ? 0 : 1) && n_chunks > 0) {
-    if (tid == 0) atomicAdd(queue_len + 1, 1);  // fallback workgroups, for tests
-    reload_q(bq);
+  // --- Fallback: pass 2 streams every chunk again for queries the decision
+  // above left unsettled. A workgroup of the first kernel with at most
+  // kInWg of them streams again itself (for all its queries); one with
+  // more hands them to gate_fallback_kernel, whose tiles hold only such
+  // queries (FB). Each score above the lane's threshold (rare: theta sits
+  // about one key below L) is appended, with its block id, to the lane's
+  // LDS buffer; a buffer that may overflow on the next chunk is folded
+  // into the lane's list of its M best, and the threshold rises to the
+  // last entry's score.
+  constexpr int kInWg = 4;
+  const int n_uns =
+      FB ? 0 : __syncthreads_count((live && half == 0 && !ok && n_chunks > 0) ? 1 : 0);
+  const bool in_wg = !FB && n_uns > 0 && n_uns <= kInWg;
+  if ((FB || in_wg) && n_chunks > 0) {
+    if (FB && tid == 0) atomicAdd(queue_len + 1, 1);  // fallback tiles, for tests
+    if (in_wg) reload_q(bq);
     clear_lists();
     float thr = thr0;
     int cnt = 0;
     auto fold = [&]() {
-      for (int e = 0; e < cnt; ++e) insert_approx<M>(lv, li, sv[e * 64], si[e * 64]);
+      for (int e = 0; e < cnt; ++e) {
+        const float x = sv[e * 64];
+        if constexpr (FB)
+          insert_keyed<M>(lk, lv, li, Elem<T>::round(x + widen(x)), x, si[e * 64]);
+        else
+          insert_approx<M>(lv, li, x, si[e * 64]);
+      }
       cnt = 0;
+      // A full list takes a later score only if it can beat the last entry.
+      // By (key, id): x + w(x) and the rounding rise with x, so x <= the
+      // last entry's score cannot reach a larger key, and a later id loses
+      // a tie.
       if (lv[M - 1] > -INFINITY) thr = fmaxf(thr0, lv[M - 1]);
     };
     // Scores go in groups of four consecutive blocks. A group is skipped
@@ -1122,18 +1345,29 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       if (__any(cnt > CAP - 16)) fold();
     });
     fold();
-    int n_in_list = 0;
+    if constexpr (FB) {
+      ok = decide_keyed();
+    } else {
+      int n_in_list = 0;
 #pragma unroll
-    for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
-    rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
-    ok = decide();
+      for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
+      rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
+      ok = decide_value();
+    }
   }
 
   if (!live || half != 0) return;
   const int64_t qid = hm_query(packed, r, hq, h_q, S, tok, t);
   if (!ok) {
-    const int slot = atomicAdd(queue_len, 1);
-    queue[slot] = (r * h_q + hq) * rows_per_seq + t;
+    if (!FB && !in_wg && n_chunks > 0) {
+      // The fallback kernel streams again for the queries that need it.
+      const int64_t li = rh * kFbBuckets + t / fb.cap;
+      const int e = atomicAdd(fb.count + li, 1);
+      fb.list[li * fb.cap + e] = make_int2(static_cast<int>(t), __float_as_int(theta));
+    } else {
+      const int slot = atomicAdd(queue_len, 1);
+      queue[slot] = (r * h_q + hq) * rows_per_seq + t;
+    }
     return;
   }
   int n_sel = 0;
@@ -1145,6 +1379,48 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     n_sel += in ? 1 : 0;
   }
   emit_sorted<TS>(sel, n_sel, own, cur != 0, out + qid * slots, slots);
+}
+
+// First kernel: one tile per workgroup, tiles numbered from the end so the
+// longest ones start first.
+template <typename T, int D, int M, int K, int CAP, int WAVES, int GB>
+__global__ void __launch_bounds__(WAVES * 64, M <= 12 ? (D == 64 ? 3 : 2) : 1)
+gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
+                 int32_t* __restrict__ out, const int32_t* __restrict__ cu,
+                 int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
+                 int take, int cur, int slots, const float* __restrict__ kbar_norm,
+                 int64_t* __restrict__ queue, int* __restrict__ queue_len,
+                 int64_t rows_per_seq, FbLists fb) {
+  const int64_t n_tiles = (rows_per_seq + 32 * WAVES - 1) / (32 * WAVES);
+  const int64_t tile = n_tiles - 1 - blockIdx.x;
+  gate_tile<T, D, M, K, CAP, WAVES, GB, false>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
+                                               take, cur, slots, kbar_norm, queue, queue_len,
+                                               rows_per_seq, blockIdx.y, tile * 32 * WAVES, fb,
+                                               nullptr, 0);
+}
+
+// Fallback kernel: the unsettled queries of one (row, query head, position
+// bucket) list per grid row, 32 * WAVES per tile, the workgroups of a row
+// striding over its tiles. The work is proportional to the unsettled
+// queries, not to the tiles that hold one.
+template <typename T, int D, int M, int K, int CAP, int WAVES, int GB>
+__global__ void __launch_bounds__(WAVES * 64, M <= 12 ? (D == 64 ? 3 : 2) : 1)
+gate_fallback_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
+                     int32_t* __restrict__ out, const int32_t* __restrict__ cu,
+                     int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
+                     int take, int cur, int slots, const float* __restrict__ kbar_norm,
+                     int64_t* __restrict__ queue, int* __restrict__ queue_len,
+                     int64_t rows_per_seq, FbLists fb) {
+  const int64_t li = blockIdx.y;
+  const int n = fb.count[li];
+  const int2* ent = fb.list + li * fb.cap;
+  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * 32 * WAVES; e0 < n;
+       e0 += static_cast<int64_t>(gridDim.x) * 32 * WAVES) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    gate_tile<T, D, M, K, CAP, WAVES, GB, true>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
+                                                take, cur, slots, kbar_norm, queue, queue_len,
+                                                rows_per_seq, li / kFbBuckets, e0, fb, ent, n);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1270,14 +1546,26 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
   // Groups tracked per lane (2K >= take). With 8, a query on i.i.d. keys
   // finds its candidates outside the kept groups about once in 4e4.
   constexpr int K = M <= 12 ? 8 : 16;
+  const FbLists fb{ws.fb_list, ws.fb_count, ws.fb_cap};
   dim3 grid(static_cast<unsigned>(cdiv(g.rows_per_seq, 32 * WAVES)),
             static_cast<unsigned>(g.rows * g.h_q));
   hipLaunchKernelGGL((gate_mfma_kernel<T, D, M, K, CAP, WAVES, GB>), grid, dim3(64 * WAVES), 0, st,
                      static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
                      g.seq_len, g.h_q, g.h_kv, g.n_blocks, static_cast<int>(g.block_size),
                      take, cur, static_cast<int>(g.slots), ws.kbar_norm, ws.queue,
-                     ws.counter, g.rows_per_seq);
-  return check_launch("moba_gate (mfma)");
+                     ws.counter, g.rows_per_seq, fb);
+  int rc = check_launch("moba_gate (mfma)");
+  if (rc) return rc;
+  // Up to 32 workgroups per list, each striding over the list's tiles; a
+  // workgroup past its list's length exits at once.
+  const int64_t per_list = cdiv(ws.fb_cap, 32 * WAVES) < 32 ? cdiv(ws.fb_cap, 32 * WAVES) : 32;
+  dim3 fgrid(static_cast<unsigned>(per_list), static_cast<unsigned>(g.rows * g.h_q * kFbBuckets));
+  hipLaunchKernelGGL((gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB>), fgrid, dim3(64 * WAVES),
+                     0, st, static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
+                     g.seq_len, g.h_q, g.h_kv, g.n_blocks, static_cast<int>(g.block_size),
+                     take, cur, static_cast<int>(g.slots), ws.kbar_norm, ws.queue,
+                     ws.counter, g.rows_per_seq, fb);
+  return check_launch("moba_gate (fallback)");
 }
 
 template <typename T>
@@ -1292,14 +1580,13 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   const bool mfma_ok = (g.head_dim == 64 || g.head_dim == 128) && take <= 16 &&
                        g.n_blocks <= 65535;
   if (!mfma_ok) return dispatch_exact<T>(q, kbar, out, cu, g, take, cur, nullptr, nullptr, st);
-  const int64_t qcap = g.rows * g.h_q * g.rows_per_seq;
+  GateWs ws = gate_ws(workspace, g.rows * g.h_kv, g.rows * g.h_q, g.rows_per_seq);
   if (!workspace || ws_bytes < moba_gate_workspace_size(g.rows, g.rows_per_seq, g.h_q) ||
-      ws_bytes < 256 + align256(sizeof(float) * g.rows * g.h_kv) + sizeof(int64_t) * qcap)
+      ws_bytes < ws.bytes)
     return fail(MOBA_ERR_WORKSPACE, "gate workspace too small");
-  GateWs ws = gate_ws(workspace, g.rows, g.h_kv, qcap);
   unsigned* norm_bits = reinterpret_cast<unsigned*>(ws.kbar_norm);
   hipLaunchKernelGGL(gate_init_kernel, dim3(1), dim3(256), 0, st, norm_bits,
-                     g.rows * g.h_kv, ws.counter);
+                     g.rows * g.h_kv, ws.counter, ws.fb_count, g.rows * g.h_q * kFbBuckets);
   hipLaunchKernelGGL(gate_prep_kernel<T>,
                      dim3(static_cast<unsigned>(cdiv(g.n_blocks * 8, 256) < 16 ? cdiv(g.n_blocks * 8, 256) : 16),
                           static_cast<unsigned>(g.rows * g.h_kv)),
@@ -1334,9 +1621,8 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
 }  // namespace moba
 
 extern "C" size_t moba_gate_workspace_size(int64_t batch, int64_t seq_len, int64_t h_q) {
-  // counter + norms (bounded by batch * h_q floats) + one queue entry per query.
-  size_t norms = (sizeof(float) * batch * h_q + 255) & ~size_t(255);
-  return 256 + norms + sizeof(int64_t) * static_cast<size_t>(batch * h_q * seq_len);
+  // The layout of moba::gate_ws with the norms bounded by batch * h_q.
+  return moba::gate_ws(nullptr, batch * h_q, batch * h_q, seq_len).bytes;
 }
 
 // ---------------------------------------------------------------------------
@@ -1348,9 +1634,16 @@ extern "C" size_t moba_gate_workspace_size(int64_t batch, int64_t seq_len, int64
 // ---------------------------------------------------------------------------
 namespace moba {
 
-constexpr size_t kStaticNormBytes = sizeof(float) * MOBA_GATE_STATIC_MAX_NORMS;
+// The gate_ws layout at its largest: norms and fallback lengths for
+// MOBA_GATE_STATIC_MAX_NORMS pairs, queue entries for the queries, and
+// fallback lists rounded up to whole buckets (at most kFbBuckets - 1 spare
+// entries per pair).
 constexpr size_t kStaticBytes =
-    256 + kStaticNormBytes + sizeof(int64_t) * size_t(MOBA_GATE_STATIC_MAX_QUERIES);
+    256 + sizeof(float) * MOBA_GATE_STATIC_MAX_NORMS +
+    sizeof(int64_t) * size_t(MOBA_GATE_STATIC_MAX_QUERIES) + 256 +
+    sizeof(int) * kFbBuckets * size_t(MOBA_GATE_STATIC_MAX_NORMS) + 256 +
+    sizeof(int2) * (size_t(MOBA_GATE_STATIC_MAX_QUERIES) +
+                    size_t(kFbBuckets - 1) * MOBA_GATE_STATIC_MAX_NORMS);
 
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 

@@ -9,9 +9,10 @@ Per case: every query of head 0 and every eighth query (a different phase
 per head, so every 128-query workgroup is covered) of the other heads are
 compared with `oracle.c_oracle.gate_select_strided` (semantics
 src/moba/naive.py:64-146), exactly. The gate's workspace counters say which
-decision path ran: offset keys must send workgroups down the fallback
-stream (the settle/fallback logic depends on the block count, and this is
-its heaviest regime), and ties to the exact queue kernel.
+decision path ran: offset keys must send queries to the fallback kernel
+(the settle/fallback logic depends on the block count, and this is its
+heaviest regime), whose (key, id)-ordered lists settle the ties; what it
+cannot settle goes on to the exact queue kernel.
 """
 
 import pytest
@@ -82,7 +83,7 @@ def test_gate_headline_whole_heads_match_oracle(device, kind, dtype, top_k):
     del k
     got, queued, fallback = _gate_with_counters(q, kbar, cfg)
     print(f"[gate-512k] {kind} {dtype} top_k={top_k}: queued {queued}, "
-          f"fallback workgroups {fallback}", flush=True)
+          f"fallback tiles {fallback}", flush=True)
     qc, kc = q.cpu(), kbar.cpu()
     del q, kbar
     ocfg = oracle_cfg(cfg)
@@ -96,4 +97,4 @@ def test_gate_headline_whole_heads_match_oracle(device, kind, dtype, top_k):
     if kind == "offset":
         # The regime this test exists for: near-tied boundary keys that the
         # one-stream decision cannot settle.
-        assert fallback > 0, "offset keys did not reach the fallback stream"
+        assert fallback > 0, "offset keys did not reach the fallback kernel"
