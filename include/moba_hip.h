@@ -114,8 +114,8 @@ int moba_gate_refine(const void* q, const void* kbar, const int32_t* super_idx,
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference.
  * Same arguments, semantics and output as moba_gate; its scratch (queue
- * counter, kbar norms, one 8-byte queue entry per query) is a static device
- * array of about 16 MiB that each GPU the library runs on holds until the
+ * counter, kbar norms, one 8-byte queue entry and one 8-byte fallback-list
+ * entry per query) is a static device array of about 33 MiB that each GPU the library runs on holds until the
  * process ends. Limits: batch * h_q * rows_per_seq <=
  * MOBA_GATE_STATIC_MAX_QUERIES and batch * h_q <= MOBA_GATE_STATIC_MAX_NORMS
  * (rows_per_seq = seq_len, or max_seqlen when packed); larger calls return
