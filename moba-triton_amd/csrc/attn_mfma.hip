@@ -502,29 +502,40 @@ bwd_mfma_kernel(AttnArgs a) {
   for (int dt = 0; dt < DT; ++dt) { dv[dt] = floatx16_t{}; dk[dt] = floatx16_t{}; }
   A* dq_out = static_cast<A*>(a.part_acc);
 
-  // Entry pipeline. Every thread tracks entry tid % NQ of a step (lanes past
-  // NQ duplicate it), so all global loads are unconditional and the wait
-  // counts stay static: while step g is computed, the Q / dO rows and
-  // lse / delta of step g + 1 and the index entries of step g + 2 are in
-  // flight; everything is waited for once, before the step's stores.
+  // Entry pipeline. A thread of the stream's first wave tracks entry
+  // stid % NQ of a step (lanes past NQ duplicate it); its loads are
+  // unconditional within the loop: while step g is computed, the Q / dO
+  // rows and lse / delta of step g + 1 and the index entries of step g + 2
+  // are in flight; everything is waited for once, after the step's dQ.
   constexpr int CH = NQ * D / 8 / NT;  // 16-byte chunks per thread per tensor
   static_assert(NQ * D / 8 % NT == 0, "row chunks must tile the workgroup");
   const int qi = stid % NQ;
   const int32_t last = c.n > 0 ? c.n - 1 : 0;
-  int32_t i_row = 0, i_head = 0, i_slot = -1;   // raw entry, step g + 2
+  int32_t i_row = 0, i_head = 0, i_slot = 0;    // raw entry, step g + 2
+  bool i_live = false;
+  // Only the first wave of a stream (threads stid < 64 >= NQ) loads the
+  // index entries and row statistics, derives them and stages them; the
+  // other waves read what it staged.
+  const bool idx_wave = stid < 64;
   auto load_idx = [&](int32_t g) {
+    if (!idx_wave) return;  // wave-uniform
     const int32_t e = g + qi;
     const int64_t i = c.lo + (e < c.n ? e : last);
     i_row = a.row_indices[i * a.istride];
     i_head = a.head_indices[i * a.istride];
-    i_slot = e < c.n ? a.slot_of_pair[i * a.istride] : -1;
+    // Raw: the entry's liveness is applied in derive(), after the wait;
+    // a select here would wait for the load right away.
+    i_slot = a.slot_of_pair[i * a.istride];
+    i_live = e < c.n;
   };
   int64_t n_pr = 0, n_dst = -1;                 // derived, step g + 1
   int n_lim = -1;
   __shared__ int64_t s_qoff_[ST][NQ];
   int64_t* s_qoff = s_qoff_[stream];
+  // derive() runs in every wave (on constants outside the first), so the
+  // loads above are consumed on every path and never waited for later.
   auto derive = [&]() {
-    const bool ok = i_slot >= 0;
+    const bool ok = i_live;
     const int64_t pr = part_row(a, c, i_row, i_head);
     const int64_t rrel = static_cast<int64_t>(i_row) - c.key0;
     const int row_lim = !a.causal ? BS : (rrel < 0 ? -1 : (rrel >= BS ? BS : static_cast<int>(rrel)));
@@ -537,9 +548,11 @@ bwd_mfma_kernel(AttnArgs a) {
   bool pv[CH];  // chunk belongs to a live entry (zeroed when staged)
   float n_lse = 0.f, n_dl = 0.f;
   auto fetch = [&]() {  // step g + 1: rows via s_qoff, lse / delta via n_pr
-    const float2 ld = *reinterpret_cast<const float2*>(a.lse_delta + 2 * n_pr);
-    n_lse = ld.x;
-    n_dl = ld.y;
+    if (idx_wave) {
+      const float2 ld = *reinterpret_cast<const float2*>(a.lse_delta + 2 * n_pr);
+      n_lse = ld.x;
+      n_dl = ld.y;
+    }
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = stid + u * NT;
@@ -650,10 +663,13 @@ bwd_mfma_kernel(AttnArgs a) {
     const bool all_visible = __all(lane >= NQ || s_lim[lane < NQ ? lane : 0] == BS - 1 ||
                                    s_lim[lane < NQ ? lane : 0] < 0);
     const bool more = g0 + ST * NQ < c.n;
-    if (more) {
-      fetch();
-      load_idx(g0 + 2 * ST * NQ);
-    }
+    // Unconditional (past the column's end they read valid, clamped rows
+    // and are never used): loads issued under a condition that the
+    // consuming derive() below repeats leave the compiler's wait analysis
+    // a path on which they are still pending at the next step, and it then
+    // waits there for every store in flight.
+    fetch();
+    load_idx(g0 + 2 * ST * NQ);
 
     // S and dP for this wave's 32 keys and each 32-query tile; lane <->
     // key, register v <-> query 32 qt + 8(v/4) + 4h + v%4.
@@ -787,10 +803,11 @@ bwd_mfma_kernel(AttnArgs a) {
           dst[t][u] = s_dst[qt * 32 + (ci >> 2)];
         }
       }
-      if (more) {
-        c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
-        derive();  // waits for every load in flight
-      }
+      // Keep the next step's index arithmetic (which waits for the loads in
+      // flight) behind this step's dQ work.
+      __builtin_amdgcn_sched_barrier(0);
+      c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
+      derive();  // waits for every load in flight
       if (next) stage(more, par ^ 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
@@ -805,10 +822,11 @@ bwd_mfma_kernel(AttnArgs a) {
       int64_t dst[TPW];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) dst[t] = s_dst[((wave + t * NW) / DT) * 32 + col];
-      if (more) {
-        c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
-        derive();
-      }
+      // Keep the next step's index arithmetic (which waits for the loads in
+      // flight) behind this step's dQ work.
+      __builtin_amdgcn_sched_barrier(0);
+      c_lim = n_lim; c_dst = n_dst; c_lse = n_lse; c_dl = n_dl;
+      derive();  // waits for every load in flight
       if (next) stage(more, par ^ 1);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
