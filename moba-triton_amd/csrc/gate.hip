@@ -866,7 +866,7 @@ __device__ __forceinline__ void gate_tile(
 
   // Lists of the fallback pass: the lane's M best candidates by (largest
   // key the score can have, id asc), approximate scores beside them.
-  float lk[FB ? M : 1], lv[M];
+  float lk[M], lv[M];  // lk: fallback kernel only
   int li[M];
   auto clear_lists = [&]() {
 #pragma unroll
