@@ -1266,7 +1266,10 @@ __device__ __forceinline__ void gate_tile(
   // LDS buffer; a buffer that may overflow on the next chunk is folded
   // into the lane's list of its M best, and the threshold rises to the
   // last entry's score.
-  constexpr int kInWg = 4;
+  // At head_dim 128 the first kernel's registers cannot hold the second
+  // stream as well (it spilled 94 dwords and ran 12% slower at config 4),
+  // so every unsettled query goes to the fallback kernel.
+  constexpr int kInWg = D == 64 ? 4 : 0;
   const int n_uns =
       FB ? 0 : __syncthreads_count((live && half == 0 && !ok && n_chunks > 0) ? 1 : 0);
   const bool in_wg = !FB && n_uns > 0 && n_uns <= kInWg;
