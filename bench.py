@@ -149,6 +149,100 @@ def summarize_counters(out_path, dbs, command):
     print(f"wrote {out_path}: {sorted(kernels)}")
 
 
+def _pmc_per_kernel(db, counter):
+    """{short kernel name: [(grid, value per dispatch), ...]} of one --pmc database."""
+    import collections
+    import sqlite3
+
+    out = collections.defaultdict(list)
+    con = sqlite3.connect(db)
+    q = ("select kernel_name, counter_name, value, grid_size, dispatch_id "
+         "from counters_collection")
+    for kname, cname, val, grid, _ in con.execute(q):
+        if cname == counter:
+            out[_short_kernel(kname)].append((int(grid), float(val)))
+    con.close()
+    return out
+
+
+def summarize_traffic(out_path, fetch_db, write_db, copy_fetch_db, copy_write_db, command):
+    """HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs
+    of the headline workload, scaled by what the same counters read for a
+    plain 1 GiB device copy (`--copy-probe`): hbm = FETCH KiB * 1024 * (copy
+    bytes / copy FETCH bytes) + WRITE KiB * 1024 * (copy bytes / copy WRITE
+    bytes). Per kernel, the average over its dispatches at the grid it has
+    at the headline size (the largest grid it ran with)."""
+    copy_bytes = 1 << 30
+
+    def copy_kib(db, counter):  # the probe's copy dispatches (not its fill)
+        vs = [v for k, d in _pmc_per_kernel(db, counter).items() if "copyBuffer" in k for _, v in d]
+        return sum(vs) / len(vs)
+
+    cf, cw = copy_kib(copy_fetch_db, "FETCH_SIZE"), copy_kib(copy_write_db, "WRITE_SIZE")
+    ff, wf = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    fetch, write = _pmc_per_kernel(fetch_db, "FETCH_SIZE"), _pmc_per_kernel(write_db, "WRITE_SIZE")
+    kernels = {}
+    for k in sorted(set(fetch) & set(write)):
+        if not k.strip() or "copyBuffer" in k:  # torch's own kernels, not the path's
+            continue
+        grid = max(g for g, _ in fetch[k])
+        fv = [v for g, v in fetch[k] if g == grid]
+        wv = [v for g, v in write[k] if g == grid]
+        if not fv or not wv:
+            continue
+        fk, wk = sum(fv) / len(fv), sum(wv) / len(wv)
+        kernels[k] = {"kernel": k, "seq_len": 524288, "grid": grid, "fetch_kib": round(fk, 1),
+                      "write_kib": round(wk, 1),
+                      "hbm_bytes_per_launch": int(fk * 1024 * ff + wk * 1024 * wf)}
+    doc = {"workload": "fwd+bwd [1,524288,4,64] bf16, block_size 128, top_k 8 (bench.py defaults)",
+           "commands": command.split(" ;; ") if command else [],
+           "calibration": {"copy_bytes_each_way": copy_bytes, "copy_fetch_kib": round(cf, 4),
+                           "copy_write_kib": round(cw, 4), "fetch_factor": round(ff, 4),
+                           "write_factor": round(wf, 4),
+                           "note": "hbm_bytes = FETCH_SIZE KiB * 1024 * fetch_factor + WRITE_SIZE "
+                                   "KiB * 1024 * write_factor, per dispatch (average over the "
+                                   "dispatches at the kernel's largest grid)"},
+           "kernels": kernels}
+    Path(out_path).write_text(json.dumps(doc, indent=1) + "\n")
+    print(f"wrote {out_path}: {sorted(kernels)}")
+
+
+def summarize_trace(out_path, db, command, bench_log):
+    """Markdown table of a rocprofv3 --kernel-trace database: per kernel
+    the calls, total and average duration over the whole run, plus the
+    bench line's step time and per-stage times when its log is given."""
+    import collections
+    import sqlite3
+
+    con = sqlite3.connect(db)
+    agg = collections.defaultdict(list)
+    for name, dur in con.execute("select name, duration from kernels"):
+        agg[name].append(dur / 1e3)
+    con.close()
+    total = sum(sum(v) for v in agg.values())
+    line = None
+    if bench_log:
+        for ln in Path(bench_log).read_text().splitlines():
+            if ln.startswith("{"):
+                line = json.loads(ln)
+    out = ["# Kernel trace: bench.py default run (fwd+bwd, S=524288, plus the S=64K..512K sweep)", "",
+           "Command (on the MI355X box, from the repo root):", "", "```", command, "```", "",
+           "Read from the run's rocpd database (`kernels` view). Durations are GPU kernel times over "
+           "the whole run (warm-up, timed steps, per-stage timing, the sweep, the hierarchical-gate "
+           "probe, the offset-key step and the other BASELINE configurations)."]
+    if line:
+        out += ["", f"Bench line of the same run: `ms_per_step` = {line['ms_per_step']}; per-stage "
+                "HIP-event medians (ms): " + ", ".join(f"{n} {r['ms']}" for n, r in
+                                                        line["stages"].items()) + "."]
+    out += ["", "| kernel | calls | total ms | avg us | % |", "|---|---:|---:|---:|---:|"]
+    for name, v in sorted(agg.items(), key=lambda x: -sum(x[1])):
+        nm = name if len(name) <= 110 else name[:107] + "..."
+        out.append(f"| `{nm}` | {len(v)} | {sum(v) / 1e3:.3f} | {sum(v) / len(v):.1f} | "
+                   f"{100 * sum(v) / total:.1f} |")
+    Path(out_path).write_text("\n".join(out) + "\n")
+    print(f"wrote {out_path}")
+
+
 def make_inputs(s, dev, seed=0):
     g = torch.Generator(device=dev).manual_seed(seed)
     shape = (1, s, HEADS, HEAD_DIM)
@@ -315,6 +409,35 @@ def hierarchical_gate(s, dev, configs=((16, 8), (4, 8)), reps=5):
     return out
 
 
+def offset_key_step(s, dev, steps=5, warmup=2):
+    """The whole fwd+bwd step (ms, wall clock between synchronizations, as the
+    headline) on keys that share one per-channel offset (3 offset + unit
+    noise, as trained keys carry): the gate's hardest distribution, beside
+    the headline's i.i.d. keys. q, v, dO as the headline."""
+    from moba.config import MoBAConfig
+    from moba.kernels.attention import moba_attention
+
+    cfg = MoBAConfig(block_size=BLOCK, top_k=TOPK)
+    q, k, v, do = make_inputs(s, dev)
+    g = torch.Generator(device=dev).manual_seed(2)
+    k = (3.0 * torch.randn((1, 1, HEADS, HEAD_DIM), generator=g, device=dev)
+         + torch.randn(k.shape, generator=g, device=dev)).to(torch.bfloat16)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        qq.grad = kk.grad = vv.grad = None
+        moba_attention(qq, kk, vv, cfg).backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return round((time.perf_counter() - t0) * 1e3 / steps, 4)
+
+
 def attainment(q, k, v, cfg, s, fwd_ms):
     """The reference's headline ratio (`bench/suite.py:1-12, 549-583`): the
     forward speedup over dense causal attention (torch SDPA, fused kernels
@@ -431,7 +554,19 @@ def main():
                     help="reduce rocprofv3 --pmc databases to OUT_JSON and exit (no GPU)")
     ap.add_argument("--command", default="", help="with --summarize-counters: the "
                     "profiling command, recorded in OUT_JSON")
+    ap.add_argument("--summarize-traffic", nargs=5,
+                    metavar=("OUT_JSON", "FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"),
+                    help="reduce FETCH_SIZE / WRITE_SIZE databases to OUT_JSON and exit (no GPU)")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("OUT_MD", "DB"),
+                    help="reduce a --kernel-trace database to OUT_MD and exit (no GPU)")
+    ap.add_argument("--bench-log", default="", help="with --summarize-trace: the run's output")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic, args.command)
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace, args.command, args.bench_log)
+        return
     if args.summarize_counters:
         summarize_counters(args.summarize_counters[0], args.summarize_counters[1:], args.command)
         return
@@ -516,6 +651,8 @@ def main():
     rows = [] if args.no_sweep else sweep(dev, SWEEP)
     hier = None if args.no_hier else hierarchical_gate(s, dev)
     torch.cuda.empty_cache()
+    offset_ms = None if args.no_hier else offset_key_step(s, dev)
+    torch.cuda.empty_cache()
     configs = [] if args.no_sweep else other_configs(dev)
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline(s, args.cpu_rows)
@@ -536,6 +673,9 @@ def main():
                           "alg_GBps": round(total_alg / (ms * 1e-3) / 1e9, 1),
                           "frac": round(total_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "stages": stage_rows,
+        # The same step on keys with a shared per-channel offset (the gate's
+        # hardest distribution), beside ms_per_step on i.i.d. keys.
+        "step_ms_by_keys": {"iid": round(ms, 4), "offset": offset_ms},
         "sweep": rows,
         "hierarchical_gate": hier,
         "other_configs": configs,
