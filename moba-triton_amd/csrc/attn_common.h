@@ -38,6 +38,8 @@ struct AttnArgs {
   int64_t seg_cap;            // entries per (row, kv head)
   float* seg_scratch;         // backward: fp32 dK / dV of cut columns' segments
   int64_t scratch_cap;        // scratch slots per (row, kv head)
+  int tile_keys;              // FMA attend: keys staged per tile when a block's K / V
+                              // exceed LDS (0: the whole block at once)
 };
 
 // Per-column context resolved from (program column position, row * h_kv).

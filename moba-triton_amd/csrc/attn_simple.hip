@@ -2,8 +2,9 @@
 //
 // This file holds the C ABI entry points of the attention stages and the
 // general kernels behind them: every dtype (the float32 path always runs
-// here), any head_dim from 8 to 256 (a multiple of 8) whose block of keys
-// and values fits in LDS at the input's width. The bf16 / fp16 MFMA kernels (attn_mfma.hip) take the shapes they
+// here), head_dim a power of two from 8 to 1024. A block whose keys and
+// values do not fit in LDS at once is staged in tiles of keys, with the
+// same arithmetic in the same order. The bf16 / fp16 MFMA kernels (attn_mfma.hip) take the shapes they
 // cover and report MOBA_ERR_UNSUPPORTED otherwise, which routes here.
 //
 // Semantics restated:
@@ -26,25 +27,30 @@
 
 namespace moba {
 
-constexpr int kE = 16;    // entries per group, forward / dq kernels
-constexpr int kBE = 32;   // entries per group, dk/dv kernel
-constexpr int kKT = 32;   // keys per tile, backward kernels
+constexpr int kE = 16;    // entries per group, forward kernel
 
 __device__ inline float neg_inf() { return -INFINITY; }
 
 // ---------------------------------------------------------------------------
 // Forward attend.
 // ---------------------------------------------------------------------------
-template <typename T, typename A>
+// TILED: the block's keys, then its values, pass through LDS a tile of
+// a.tile_keys at a time (head_dim above 256, or blocks too large for LDS);
+// each thread then keeps the sums of its (entry, feature) elements, at most
+// OWN of them, in registers across the tiles. Otherwise the whole block
+// stays in LDS. Both form every score, max, sum and product in the same
+// order, so their results are identical.
+template <typename T, typename A, bool TILED, int OWN>
 __global__ void __launch_bounds__(256)
 attend_simple_kernel(AttnArgs a) {
   extern __shared__ float smem[];
   const int64_t D = a.D, bs = a.bs;
+  const int64_t KT = TILED ? a.tile_keys : bs;
   // The block's keys and values stay in the input type (16-bit types take
-  // half the LDS, so a 128-key block of head_dim 256 fits).
-  T* Ks = reinterpret_cast<T*>(smem);  // [bs][D]
-  T* Vs = Ks + bs * D;                 // [bs][D]
-  float* Qs = reinterpret_cast<float*>(Vs + bs * D);  // [kE][D]
+  // half the LDS, so a 128-key block of head_dim 256 fits whole).
+  T* Ks = reinterpret_cast<T*>(smem);      // [KT][D]
+  T* Vs = TILED ? Ks : Ks + bs * D;        // [bs][D] (TILED: the same tile)
+  float* Qs = reinterpret_cast<float*>(Ks + (TILED ? KT : 2 * bs) * D);  // [kE][D]
   float* Ss = Qs + kE * D;          // [kE][bs]
   float* Ms = Ss + kE * bs;         // [kE]
   float* Ls = Ms + kE;              // [kE]
@@ -57,12 +63,17 @@ attend_simple_kernel(AttnArgs a) {
   const T* K = static_cast<const T*>(a.k);
   const T* V = static_cast<const T*>(a.v);
   const T* Q = static_cast<const T*>(a.q);
-  for (int64_t i = threadIdx.x; i < bs * D; i += blockDim.x) {
-    const int64_t j = i / D, d = i % D;
-    const bool ok = c.key0 + j < c.key_end;
-    const int64_t off = ((c.tok0 + j) * a.h_kv + c.hk) * D + d;
-    Ks[i] = ok ? K[off] : T{};
-    Vs[i] = ok ? V[off] : T{};
+  // Keys kt0 .. kt0 + KT - 1 of `src` into `dst` (zero past the block).
+  auto stage = [&](T* dst, const T* src, int64_t kt0) {
+    for (int64_t i = threadIdx.x; i < KT * D; i += blockDim.x) {
+      const int64_t j = kt0 + i / D, d = i % D;
+      const bool ok = j < bs && c.key0 + j < c.key_end;
+      dst[i] = ok ? src[((c.tok0 + j) * a.h_kv + c.hk) * D + d] : T{};
+    }
+  };
+  if constexpr (!TILED) {
+    stage(Ks, K, 0);
+    stage(Vs, V, 0);
   }
   for (int32_t e0 = 0; e0 < c.n; e0 += kE) {
     __syncthreads();
@@ -80,17 +91,24 @@ attend_simple_kernel(AttnArgs a) {
       Qs[i] = Rs[e] >= 0 ? Elem<T>::load(Q, q_offset(a, c, Rs[e], Hs[e]) + d) : 0.f;
     }
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < kE * bs; i += blockDim.x) {
-      const int e = static_cast<int>(i / bs);
-      const int64_t j = i % bs;
-      const int64_t kpos = c.key0 + j;
-      float s = 0.f;
-      for (int64_t d = 0; d < D; ++d) s = fmaf(Qs[e * D + d], Elem<T>::load(Ks, j * D + d), s);
-      s *= a.scale_log2;
-      const bool ok = kpos < c.key_end && (!a.causal || kpos <= Rs[e]);
-      Ss[i] = ok ? s : neg_inf();
+    for (int64_t kt0 = 0; kt0 < bs; kt0 += KT) {
+      if constexpr (TILED) {
+        stage(Ks, K, kt0);
+        __syncthreads();
+      }
+      for (int64_t i = threadIdx.x; i < kE * KT; i += blockDim.x) {
+        const int e = static_cast<int>(i / KT);
+        const int64_t jt = i % KT, j = kt0 + jt;
+        if (j >= bs) continue;
+        const int64_t kpos = c.key0 + j;
+        float s = 0.f;
+        for (int64_t d = 0; d < D; ++d) s = fmaf(Qs[e * D + d], Elem<T>::load(Ks, jt * D + d), s);
+        s *= a.scale_log2;
+        const bool ok = kpos < c.key_end && (!a.causal || kpos <= Rs[e]);
+        Ss[e * bs + j] = ok ? s : neg_inf();
+      }
+      __syncthreads();
     }
-    __syncthreads();
     if (threadIdx.x < kE) {
       const int e = threadIdx.x;
       float m = neg_inf();
@@ -110,14 +128,51 @@ attend_simple_kernel(AttnArgs a) {
     }
     __syncthreads();
     A* acc_out = static_cast<A*>(a.part_acc);
-    for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
-      const int e = static_cast<int>(i / D);
-      const int64_t d = i % D;
-      if (Rs[e] < 0) continue;
-      float acc = 0.f;
-      for (int64_t j = 0; j < bs; ++j) acc = fmaf(Ss[e * bs + j], Elem<T>::load(Vs, j * D + d), acc);
-      const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
-      Elem<A>::store(acc_out, dst * D + d, acc);
+    if constexpr (!TILED) {
+      for (int64_t i = threadIdx.x; i < kE * D; i += blockDim.x) {
+        const int e = static_cast<int>(i / D);
+        const int64_t d = i % D;
+        if (Rs[e] < 0) continue;
+        float acc = 0.f;
+        for (int64_t j = 0; j < bs; ++j) acc = fmaf(Ss[e * bs + j], Elem<T>::load(Vs, j * D + d), acc);
+        const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
+        Elem<A>::store(acc_out, dst * D + d, acc);
+      }
+    } else {
+      // Element i = threadIdx.x + 256 u of the group's [kE][D] outputs (kE * D
+      // is a multiple of 256 at the head_dims that take this path).
+      const int own = static_cast<int>(kE * D / 256);
+      float acc[OWN];
+#pragma unroll
+      for (int u = 0; u < OWN; ++u) acc[u] = 0.f;
+      for (int64_t kt0 = 0; kt0 < bs; kt0 += KT) {
+        __syncthreads();  // the previous tile (or the keys) fully read
+        stage(Vs, V, kt0);
+        __syncthreads();
+        const int64_t kn = kt0 + KT < bs ? KT : bs - kt0;
+#pragma unroll
+        for (int u = 0; u < OWN; ++u) {
+          if (u < own) {
+            const int64_t i = threadIdx.x + 256 * static_cast<int64_t>(u);
+            const int e = static_cast<int>(i / D);
+            const int64_t d = i % D;
+            float x = acc[u];
+            for (int64_t jt = 0; jt < kn; ++jt)
+              x = fmaf(Ss[e * bs + kt0 + jt], Elem<T>::load(Vs, jt * D + d), x);
+            acc[u] = x;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < OWN; ++u) {
+        const int64_t i = threadIdx.x + 256 * static_cast<int64_t>(u);
+        const int e = static_cast<int>(i / D);
+        const int64_t d = i % D;
+        if (u < own && Rs[e] >= 0) {
+          const int64_t dst = part_row(a, c, Rs[e], Hs[e]) * a.slots + Zs[e];
+          Elem<A>::store(acc_out, dst * D + d, acc[u]);
+        }
+      }
     }
   }
 }
@@ -125,7 +180,9 @@ attend_simple_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Backward: dK / dV per key tile, one program per (column, key tile).
 // ---------------------------------------------------------------------------
-template <typename T, int MAXD>
+// KT keys per tile, BE entries per group; the tile sizes shrink with
+// head_dim so the float32 tiles fit in LDS.
+template <typename T, int MAXD, int kKT, int kBE>
 __global__ void __launch_bounds__(256)
 bwd_dkdv_simple_kernel(AttnArgs a) {
   extern __shared__ float smem[];
@@ -235,7 +292,8 @@ bwd_dkdv_simple_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Backward: per-slot dQ partials, one program per column.
 // ---------------------------------------------------------------------------
-template <typename T, typename A, int MAXD>
+// kKT keys per tile, kE entries per group, as the dK / dV kernel.
+template <typename T, typename A, int MAXD, int kKT, int kE>
 __global__ void __launch_bounds__(256)
 bwd_dq_simple_kernel(AttnArgs a) {
   extern __shared__ float smem[];
@@ -447,9 +505,10 @@ combine_kernel(const float* __restrict__ part_ml, const A* __restrict__ part_acc
 }
 
 // delta[row] = sum_d O[row, d] * dO[row, d]. L lanes own one token-major
-// row (8 features each, one vector load per tensor), so a wave streams
-// 64 / L whole rows per instruction; the L partial sums meet by shuffles.
-template <typename T, int L>
+// row (C chunks of 8 features each, one vector load per tensor and chunk),
+// so a wave streams 64 / L whole rows per instruction; the L partial sums
+// meet by shuffles.
+template <typename T, int L, int C>
 __global__ void __launch_bounds__(256)
 delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, const float* __restrict__ lse,
              float* __restrict__ delta, int64_t n_rows, int64_t S, int64_t h_q) {
@@ -458,11 +517,14 @@ delta_kernel(const T* __restrict__ o, const T* __restrict__ dout, const float* _
   const int sub = static_cast<int>(gid % L);
   float acc = 0.f;
   if (row < n_rows) {
-    float x[8], y[8];
-    load8<T>(o + row * (8 * L) + 8 * sub, x);
-    load8<T>(dout + row * (8 * L) + 8 * sub, y);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = fmaf(x[i], y[i], acc);
+    for (int ch = 0; ch < C; ++ch) {
+      float x[8], y[8];
+      load8<T>(o + row * (8 * L * C) + 8 * (sub + L * ch), x);
+      load8<T>(dout + row * (8 * L * C) + 8 * (sub + L * ch), y);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fmaf(x[i], y[i], acc);
+    }
   }
 #pragma unroll
   for (int w = L / 2; w > 0; w >>= 1) acc += __shfl_xor(acc, w);
@@ -617,10 +679,9 @@ static int set_segments(AttnArgs* a, const int32_t* segments, const int32_t* seg
   return MOBA_OK;
 }
 
-// The FMA kernels take head_dim 8..256; the attend kernel keeps a block's
-// keys and values in LDS at the input's width.
+// The FMA kernels take head_dim 8..1024 (a power of two).
 static bool simple_shape_ok(const Geometry& g) {
-  return g.head_dim <= 256 && g.head_dim >= 8;
+  return g.head_dim <= 1024 && g.head_dim >= 8;
 }
 
 template <typename K>
@@ -683,22 +744,37 @@ extern "C" int moba_attend(const void* q, const void* k, const void* v,
   if (st != MOBA_ERR_UNSUPPORTED) return st;
   a.seg = nullptr;  // the FMA kernels take whole columns
   if (!simple_shape_ok(g))
-    return fail(MOBA_ERR_UNSUPPORTED, "attend: head_dim must be in [8, 256]");
+    return fail(MOBA_ERR_UNSUPPORTED, "attend: head_dim must be in [8, 1024]");
   const size_t esize = dtype == MOBA_FP32 ? 4 : 2;
-  const size_t lds = esize * 2 * block_size * head_dim +
-                     sizeof(float) * (kE * head_dim + kE * block_size + 2 * kE) +
-                     sizeof(int) * 3 * kE;
-  if (lds > 160 * 1024)
-    return fail(MOBA_ERR_UNSUPPORTED,
-                "attend: a block's keys and values must fit in LDS (2 * block_size * "
-                "head_dim * element bytes <= about 130000)");
+  constexpr size_t kLds = 160 * 1024;
+  // Queries, scores and row statistics of a group; then the block's keys
+  // and values whole, or tiles of keys when they do not fit.
+  const size_t fixed = sizeof(float) * (kE * head_dim + kE * block_size + 2 * kE) +
+                       sizeof(int) * 3 * kE;
+  const size_t whole = fixed + esize * 2 * block_size * head_dim;
+  int64_t kt = 0;
+  if (whole > kLds) {
+    for (kt = 1; kt * 2 <= block_size && fixed + esize * 2 * kt * head_dim <= kLds;) kt *= 2;
+    if (fixed + esize * kt * head_dim > kLds)
+      return fail(MOBA_ERR_UNSUPPORTED,
+                  "attend: a group's queries and scores exceed LDS (4 * 16 * (head_dim + "
+                  "block_size) bytes above about 160 KiB)");
+  }
+  a.tile_keys = static_cast<int>(kt);
+  const size_t lds = kt ? fixed + esize * kt * head_dim : whole;
   dim3 grid(static_cast<unsigned>(n_blocks), static_cast<unsigned>(batch * h_kv));
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
     return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
-      int rc = set_lds(attend_simple_kernel<T, A>, lds);
-      if (rc) return rc;
-      hipLaunchKernelGGL((attend_simple_kernel<T, A>), grid, dim3(256), lds, s, a);
-      return check_launch("moba_attend");
+      auto go = [&](auto kernel) {
+        int rc = set_lds(kernel, lds);
+        if (rc) return rc;
+        hipLaunchKernelGGL(kernel, grid, dim3(256), lds, s, a);
+        return check_launch("moba_attend");
+      };
+      if (!kt) return go(attend_simple_kernel<T, A, false, 1>);
+      if (head_dim <= 256) return go(attend_simple_kernel<T, A, true, 16>);
+      if (head_dim <= 512) return go(attend_simple_kernel<T, A, true, 32>);
+      return go(attend_simple_kernel<T, A, true, 64>);
     });
   });
 }
@@ -737,16 +813,22 @@ extern "C" int moba_bwd_delta(const void* out, const void* dout, const float* ls
     return fail(MOBA_ERR_INVALID, "non-positive shape argument");
   if (!out || !dout || !delta) return fail(MOBA_ERR_INVALID, "null pointer");
   const int64_t n_rows = batch * h_q * seq_len;
-  const int64_t lanes = head_dim / 8;
-  if (head_dim % 8 != 0 || lanes > 64 || (lanes & (lanes - 1)) != 0)
-    return fail(MOBA_ERR_UNSUPPORTED, "delta: head_dim must be 8 times a power of two <= 512");
+  const int64_t chunks = head_dim / 8;
+  if (head_dim % 8 != 0 || chunks > 128 || (chunks & (chunks - 1)) != 0)
+    return fail(MOBA_ERR_UNSUPPORTED, "delta: head_dim must be 8 times a power of two <= 1024");
+  const int64_t lanes = chunks < 64 ? chunks : 64;  // a row spans at most one wave
   dim3 grid(static_cast<unsigned>(cdiv(n_rows * lanes, 256)));
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
     auto go = [&](auto lanes_c) {
       constexpr int Lc = decltype(lanes_c)::value;
-      hipLaunchKernelGGL((delta_kernel<T, Lc>), grid, dim3(256), 0, as_stream(stream),
-                         static_cast<const T*>(out), static_cast<const T*>(dout), lse,
-                         delta, n_rows, seq_len, h_q);
+      if (Lc == 64 && chunks == 128)
+        hipLaunchKernelGGL((delta_kernel<T, 64, 2>), grid, dim3(256), 0, as_stream(stream),
+                           static_cast<const T*>(out), static_cast<const T*>(dout), lse,
+                           delta, n_rows, seq_len, h_q);
+      else
+        hipLaunchKernelGGL((delta_kernel<T, Lc, 1>), grid, dim3(256), 0, as_stream(stream),
+                           static_cast<const T*>(out), static_cast<const T*>(dout), lse,
+                           delta, n_rows, seq_len, h_q);
     };
     switch (lanes) {
       case 1: go(std::integral_constant<int, 1>{}); break;
@@ -806,13 +888,19 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
   }
   if (st != MOBA_ERR_UNSUPPORTED) return st;
   a.seg = nullptr;  // the FMA kernels take whole columns
-  if (head_dim > 256 || head_dim < 8)
-    return fail(MOBA_ERR_UNSUPPORTED, "backward: head_dim must be in [8, 256]");
-  const int64_t tiles = cdiv(block_size, kKT);
-  const size_t lds_kv = sizeof(float) * (2 * kKT * head_dim + 2 * kBE * head_dim +
-                                         2 * kBE * kKT + 2 * kBE) + sizeof(int) * 2 * kBE;
-  const size_t lds_q = sizeof(float) * (2 * kKT * head_dim + 2 * kE * head_dim +
-                                        kE * kKT + 2 * kE) + sizeof(int) * 3 * kE;
+  if (head_dim > 1024 || head_dim < 8)
+    return fail(MOBA_ERR_UNSUPPORTED, "backward: head_dim must be in [8, 1024]");
+  // Keys per tile and entries per group of the two kernels: float32 tiles
+  // of K, V, Q and dO must fit in LDS, so they shrink with head_dim.
+  const int kt_kv = head_dim <= 256 ? 32 : (head_dim <= 512 ? 16 : 8);
+  const int be_kv = kt_kv;
+  const int kt_q = kt_kv;
+  const int e_q = head_dim <= 256 ? 16 : 8;
+  const int64_t tiles = cdiv(block_size, kt_kv);
+  const size_t lds_kv = sizeof(float) * (2 * kt_kv * head_dim + 2 * be_kv * head_dim +
+                                         2 * be_kv * kt_kv + 2 * be_kv) + sizeof(int) * 2 * be_kv;
+  const size_t lds_q = sizeof(float) * (2 * kt_q * head_dim + 2 * e_q * head_dim +
+                                        e_q * kt_q + 2 * e_q) + sizeof(int) * 3 * e_q;
   return MOBA_DISPATCH_DTYPE(dtype, T, [&] {
     return MOBA_DISPATCH_ACC(acc_dtype, A, [&] {
       auto run = [&](auto dkdv_kernel, auto dq_kernel) {
@@ -832,8 +920,12 @@ extern "C" int moba_bwd(const void* q, const void* k, const void* v, const void*
         return check_launch("moba_bwd (dq)");
       };
       if (head_dim <= 128)
-        return run(bwd_dkdv_simple_kernel<T, 128>, bwd_dq_simple_kernel<T, A, 128>);
-      return run(bwd_dkdv_simple_kernel<T, 256>, bwd_dq_simple_kernel<T, A, 256>);
+        return run(bwd_dkdv_simple_kernel<T, 128, 32, 32>, bwd_dq_simple_kernel<T, A, 128, 32, 16>);
+      if (head_dim <= 256)
+        return run(bwd_dkdv_simple_kernel<T, 256, 32, 32>, bwd_dq_simple_kernel<T, A, 256, 32, 16>);
+      if (head_dim <= 512)
+        return run(bwd_dkdv_simple_kernel<T, 512, 16, 16>, bwd_dq_simple_kernel<T, A, 512, 16, 8>);
+      return run(bwd_dkdv_simple_kernel<T, 1024, 8, 8>, bwd_dq_simple_kernel<T, A, 1024, 8, 8>);
     });
   });
 }

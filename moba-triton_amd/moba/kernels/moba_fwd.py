@@ -152,10 +152,10 @@ def _validate(q, k, v, cfg: MoBAConfig, cu_seqlens=None, max_seqlen=None) -> Non
     ok, reason = check_gathered_head_dim(q.shape[-1], q.element_size())
     if not ok:
         raise ValueError(reason)
-    if q.shape[-1] > 256:
+    if q.shape[-1] > MAX_HEAD_DIM:
         # The reference admits any power of two (moba_fwd.py:774-776); the
-        # kernels here cover up to 256 (MFMA at 64 and 128, FMA beyond).
-        raise ValueError(f"head_dim {q.shape[-1]} above 256 is not supported")
+        # kernels here cover up to 1024 (MFMA at 64 and 128, FMA beyond).
+        raise ValueError(f"head_dim {q.shape[-1]} above {MAX_HEAD_DIM} is not supported")
     if cfg.block_size < TENSOR_CORE_TILE:
         raise ValueError(f"block_size {cfg.block_size} below the MFMA tile minimum "
                          f"of {TENSOR_CORE_TILE}")
@@ -165,25 +165,27 @@ def _validate(q, k, v, cfg: MoBAConfig, cu_seqlens=None, max_seqlen=None) -> Non
 
 
 # Shapes the MFMA attend kernel covers; the others run the FMA attend kernel,
-# which keeps a whole block's keys and values in LDS at the input's width.
+# which keeps a block's keys and values in LDS at the input's width, whole
+# or (when they do not fit) one tile of keys at a time.
 _MFMA_HEAD_DIMS, _MFMA_BLOCKS = (64, 128), (32, 64, 128)
 _LDS_BYTES = 160 * 1024
+MAX_HEAD_DIM = 1024
 
 
 def fits_attend_lds(head_dim: int, block_size: int, dtype) -> tuple[bool, str]:
-    """Whether a block's keys and values fit the FMA attend kernel's LDS
-    (csrc/attn_simple.hip moba_attend: 2 * block_size * head_dim * element
-    bytes plus its per-group staging, at most 160 KiB); always true where the
-    MFMA kernel takes the shape."""
+    """Whether the FMA attend kernel can run the shape (csrc/attn_simple.hip
+    moba_attend): a group's 16 float32 query rows and score rows, plus at
+    least one key row, within 160 KiB of LDS. Always true where the MFMA
+    kernel takes the shape."""
     if (dtype in (torch.bfloat16, torch.float16) and head_dim in _MFMA_HEAD_DIMS
             and block_size in _MFMA_BLOCKS):
         return True, ""
     esize = torch.empty((), dtype=dtype).element_size()
     e = 16  # queries per group of the FMA kernel
-    lds = esize * 2 * block_size * head_dim + 4 * (e * head_dim + e * block_size + 2 * e) + 4 * 3 * e
+    lds = 4 * (e * head_dim + e * block_size + 2 * e) + 4 * 3 * e + esize * head_dim
     if lds > _LDS_BYTES:
-        return False, (f"block_size {block_size} x head_dim {head_dim} in {dtype}: a block's "
-                       f"keys and values need {lds} bytes of LDS, above the {_LDS_BYTES} "
+        return False, (f"block_size {block_size} x head_dim {head_dim} in {dtype}: a group's "
+                       f"queries and scores need {lds} bytes of LDS, above the {_LDS_BYTES} "
                        f"the attend kernel has")
     return True, ""
 

@@ -185,24 +185,26 @@ def test_hierarchical_gate_config_fields():
 
 def test_validation_head_dim_range():
     cfg = MoBAConfig(block_size=128, top_k=8)
-    z = torch.zeros(1, 256, 2, 256, dtype=torch.bfloat16)
-    _validate(z, z, z, cfg)  # head_dim 256 is accepted (FMA kernels)
-    with pytest.raises(ValueError, match="above 256"):
-        z = torch.zeros(1, 256, 2, 512, dtype=torch.bfloat16)
+    for d in (256, 512, 1024):  # the FMA kernels, keys staged in tiles past 256
+        z = torch.zeros(1, 256, 2, d, dtype=torch.bfloat16)
+        _validate(z, z, z, cfg)
+    with pytest.raises(ValueError, match="above 1024"):
+        z = torch.zeros(1, 256, 2, 2048, dtype=torch.bfloat16)
         _validate(z, z, z, cfg)
 
 
 @pytest.mark.parametrize("dtype,d,bs,ok", [
-    (torch.float32, 256, 128, False),   # 256 KiB of keys and values
-    (torch.bfloat16, 256, 256, False),
-    (torch.float32, 256, 64, True),
-    (torch.bfloat16, 256, 128, True),
+    (torch.float32, 256, 128, True),    # 256 KiB of keys and values: tiles of keys
+    (torch.bfloat16, 256, 256, True),
+    (torch.float32, 1024, 512, True),
+    (torch.float32, 1024, 2048, False),  # 16 score rows of 2048 alone exceed LDS
     (torch.bfloat16, 128, 128, True),   # MFMA kernel
 ])
 def test_validation_rejects_blocks_beyond_lds(dtype, d, bs, ok):
-    """The FMA attend kernel holds a block's keys and values in LDS: a shape
-    that cannot fit is a ValueError before any launch, not a failure inside
-    the library call."""
+    """The FMA attend kernel stages a block's keys and values in tiles when
+    they do not fit in LDS whole, but a group's 16 query rows and score rows
+    must fit: a shape beyond that is a ValueError before any launch, not a
+    failure inside the library call."""
     cfg = MoBAConfig(block_size=bs, top_k=2, dtype=dtype)
     z = torch.zeros(1, 4 * bs, 2, d, dtype=dtype)
     if ok:

@@ -420,14 +420,19 @@ def test_cut_columns_equal_whole_columns(device, monkeypatch, shape, h_kv, cu):
     assert torch.equal(cut[3], again[3]) and torch.equal(cut[4], again[4])
 
 
-@pytest.mark.parametrize("dtype,bs", [(torch.bfloat16, 128), (torch.float16, 64),
-                                      (torch.float32, 64)])
-def test_head_dim_256_forward_and_backward(device, dtype, bs):
-    """head_dim 256 (admitted by the reference's _validate, moba_fwd.py:774-776)
-    runs on the FMA kernels: forward and gradients against fp64 autograd of
-    the oracle, under the dtype's bar."""
+@pytest.mark.parametrize("dtype,bs,d", [
+    (torch.bfloat16, 128, 256), (torch.float16, 64, 256), (torch.float32, 64, 256),
+    # a block's keys and values beyond LDS: staged in tiles of keys
+    (torch.float32, 128, 256), (torch.bfloat16, 256, 256),
+    (torch.bfloat16, 128, 512), (torch.float32, 64, 512),
+    (torch.bfloat16, 64, 1024), (torch.float32, 32, 1024)])
+def test_large_head_dim_forward_and_backward(device, dtype, bs, d):
+    """head_dim 256 to 1024 (the reference's _validate admits any power of
+    two, moba_fwd.py:774-776) runs on the FMA kernels, whose key tiles shrink
+    with head_dim: forward and gradients against fp64 autograd of the
+    oracle, under the dtype's bar."""
     cfg = MoBAConfig(block_size=bs, top_k=4, dtype=dtype)
-    shape = (1, 1024, 2, 256)
+    shape = (1, 1024, 2, d)
     q, k, v = make_qkv(shape, dtype, seed=31, device=device)
     g = make_qkv(shape, dtype, seed=32, device=device, n=1)[0]
     sel = oracle_selection(q, k, cfg)
