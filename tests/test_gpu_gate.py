@@ -248,3 +248,80 @@ def test_gate_fallback_settles_heavy_ties_exactly(device, dtype):
     ref = c_oracle.gate_select(q.cpu(), kbar.cpu(), oracle_cfg(cfg))
     bad = (out.cpu() != ref).any(-1)
     assert not bool(bad.any()), f"{int(bad.sum())} queries differ"
+
+
+def _gate_with_counters(q, kbar, cfg, cu=None, mx=None):
+    """moba_gate with its own workspace: the ids and the workspace's two
+    counters (queries sent to the exact queue, tiles the fallback kernel
+    ran)."""
+    from moba import _lib
+
+    b, s, h, d = q.shape
+    rows = s if cu is None else mx          # rows per sequence
+    seqs = b if cu is None else cu.numel() - 1  # the C call's batch: sequences when packed
+    n = kbar.shape[2]
+    ws = torch.zeros(int(_lib.load().moba_gate_workspace_size(seqs, rows, h)),
+                     dtype=torch.uint8, device=q.device)
+    out = torch.full((b, h, s, cfg.slots()), -7, dtype=torch.int32, device=q.device)
+    take = cfg.past_blocks_selected(-(-rows // cfg.block_size))
+    _lib.call("moba_gate", _lib.ptr(q), _lib.ptr(kbar), _lib.ptr(out),
+              None if cu is None else _lib.ptr(cu), seqs, s, rows, h, kbar.shape[1], d, n,
+              cfg.block_size, cfg.slots(), take, int(bool(cfg.always_select_current)),
+              _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws.numel(), _lib.stream_handle(q.device))
+    torch.cuda.synchronize()
+    queued, tiles = ws[:8].view(torch.int32).tolist()
+    return out, queued, tiles
+
+
+def _heavy_tie_keys(shape, dtype, seed, device):
+    """One shared per-channel offset, 8 times the noise: scores take only a
+    few rounded values, so many queries of a workgroup stay unsettled."""
+    g = torch.Generator().manual_seed(seed)
+    k = 8.0 * torch.randn((1, 1) + tuple(shape[2:]), generator=g) + torch.randn(shape, generator=g)
+    return k.to(dtype).to(device)
+
+
+@pytest.mark.parametrize("case", ["packed_gqa", "d128", "take16_bs32", "multi_tile_lists"])
+def test_gate_fallback_kernel_paths_match_oracle(device, case):
+    """Shared-offset keys leave many queries of a workgroup unsettled, so the
+    first kernel hands them to the fallback kernel (its tile counter is
+    non-zero): through packed sequences with grouped query heads, at head
+    dim 128 (where every unsettled query goes there), at take 16 with
+    32-key blocks, and with lists long enough that several tiles of one
+    list are spread over the workgroups striding over it. Every id as the
+    oracle selects it."""
+    dtype = torch.bfloat16
+    cu = mx = None
+    if case == "packed_gqa":
+        cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
+        lens = [8192, 517, 6000, 1200]
+        cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32,
+                          device=device)
+        mx = max(lens)
+        t = int(cu[-1])
+        q = make_qkv((1, t, 4, 64), dtype, seed=41, device=device, n=1)[0]
+        k = _heavy_tie_keys((1, t, 2, 64), dtype, 42, device)
+    elif case == "d128":
+        cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
+        q = make_qkv((1, 8192, 2, 128), dtype, seed=43, device=device, n=1)[0]
+        k = _heavy_tie_keys((1, 8192, 2, 128), dtype, 44, device)
+    elif case == "take16_bs32":
+        cfg = MoBAConfig(block_size=32, top_k=17, dtype=dtype)
+        q = make_qkv((1, 8192, 2, 64), dtype, seed=45, device=device, n=1)[0]
+        k = _heavy_tie_keys((1, 8192, 2, 64), dtype, 46, device)
+    else:
+        cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
+        q = make_qkv((1, 65536, 2, 64), dtype, seed=47, device=device, n=1)[0]
+        k = _heavy_tie_keys((1, 65536, 2, 64), dtype, 48, device)
+    kbar = pool_blocks(k, cfg, cu_seqlens=cu, max_seqlen=mx)
+    got, queued, tiles = _gate_with_counters(q, kbar, cfg, cu, mx)
+    print(f"[fallback paths] {case}: fallback tiles {tiles}, queued {queued}", flush=True)
+    ref = c_oracle.gate_select(q.cpu(), kbar.cpu(), oracle_cfg(cfg),
+                               None if cu is None else cu.cpu(), mx)
+    bad = (got.cpu() != ref).any(-1)
+    assert not bool(bad.any()), (
+        f"{int(bad.sum())} queries route differently; first {torch.nonzero(bad)[0].tolist()}")
+    assert tiles > 0, "no query reached the fallback kernel"
+    if case == "multi_tile_lists":
+        # 2 heads x 16 buckets: more tiles than lists means lists of several tiles
+        assert tiles > 2 * 16, tiles
