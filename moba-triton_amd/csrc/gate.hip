@@ -24,9 +24,9 @@
 //     bound on L (the take-th best of all); theta lies just below the
 //     scores that can round to the key R(bound - w) or above (every
 //     selected key is at least that).
-//   - Decide: |approx - exact| <= E with E = 2^-14 |q| max|kbar| plus the
-//     denormal terms (any float32 sum of D <= 128 products is within
-//     D 2^-24 |q| |kbar|), so a score's key (the exact score rounded to
+//   - Decide: |approx - exact| <= E with E = D 2^-22 |q| max|kbar| plus
+//     the denormal terms (twice the D 2^-23 |q| |kbar| that D float32
+//     additions rounding by at most one ulp each can lose), so a score's key (the exact score rounded to
 //     float32 and to the dtype) lies in [R(a - w), R(a + w)], w being E
 //     widened by float32 rounding. The candidates (scores >= theta of the
 //     kept groups) are compacted per lane; those with a single possible
@@ -668,12 +668,17 @@ __device__ __forceinline__ void gate_tile(
   qn += __shfl_xor(qn, 32);
   // Accumulation error, plus what flushing denormal operands could drop:
   // each flushed factor is below kDenorm and its partner below |q| or |kbar|.
+  // The products of 16-bit inputs are exact in float32; the D of them reach
+  // the result through at most D float32 additions, in any order, each
+  // rounding by at most one ulp (2^-23 relative, truncation included) of a
+  // partial sum no larger than sum |q_i kbar_i| <= |q| |kbar|. So
+  // |approx - exact| <= D 2^-23 |q| |kbar|; E takes twice that.
   const float qnorm = sqrtf(qn) * 1.0001f;
   // Slack for the float sum of squares and sqrtf (a few ulp).
   const float knorm = kbar_norm[r * h_kv + hk] * 1.0001f + 1e-30f;
   // The last term covers float32 denormal products or partial sums the
   // matrix core may flush: at most 2^-126 each, D + 1 of them.
-  const float E = ldexpf(qnorm * knorm, -14) + Ops::kDenorm * D * (qnorm + knorm) +
+  const float E = qnorm * knorm * (D * 0x1p-22f) + Ops::kDenorm * D * (qnorm + knorm) +
                   (D + 1) * 1.2e-38f;
   // E widened by the float32 rounding of a -+ E (2.4e-7 > 2^-22).
   auto widen = [&](float a) { return E * 1.001f + fabsf(a) * 2.4e-7f; };
@@ -1124,6 +1129,7 @@ __device__ __forceinline__ void gate_tile(
   constexpr int C = CB < 24 ? CB : 24;
   static_assert(C >= 4, "candidate buffer");
   float* cbuf = reinterpret_cast<float*>(&s_kb[0][0]) + wave * (C + 1) * 64 + lane;
+  uint32_t* su_c = reinterpret_cast<uint32_t*>(cbuf);
   auto widen_c = [&](float a) { return widen(a) + fabsf(a) * ldexpf(1.f, IB - 22); };
   int cn = 0;
   // Largest candidate score that found the buffer full (groups come in
@@ -1202,24 +1208,25 @@ __device__ __forceinline__ void gate_tile(
 #pragma unroll
     for (int p = 0; p < TS; ++p) pkl[p] = __shfl_xor(kl[p], 32);
     const float kappa = take > 0 ? kth_of_union<TS>(kl, pkl, take) : -INFINITY;
-    const int ns_pair = max(ns, __shfl_xor(ns, 32));
+    // The straddlers that reach kappa, as block ids at the front of the
+    // buffer (in place: entry nr is written after entry e >= nr is read).
+    int nr = 0;
+    for (int e = 0; e < ns; ++e) {
+      float x, klo, khi;
+      int jx;
+      cand(e, x, jx, klo, khi);
+      if (!(khi < kappa)) {
+        su_c[nr * 64] = static_cast<uint32_t>(jx);
+        ++nr;
+      }
+    }
+    const int nr_pair = max(nr, __shfl_xor(nr, 32));
     V qv[KSTEPS];
-    bool q_loaded = false;  // wave-uniform
+    if (__any(ok && nr_pair > 0)) reload_q(qv);
 #pragma unroll 1
-    for (int e = 0; ok && e < ns_pair; ++e) {
-      int jm = -1;
-      if (e < ns) {
-        float x, klo, khi;
-        int jx;
-        cand(e, x, jx, klo, khi);
-        if (!(khi < kappa)) jm = jx;
-      }
+    for (int e = 0; ok && e < nr_pair; ++e) {
+      const int jm = e < nr ? static_cast<int>(su_c[e * 64]) : -1;
       const int jp = __shfl_xor(jm, 32);
-      if (!__any(jm >= 0)) continue;
-      if (!q_loaded) {
-        reload_q(qv);
-        q_loaded = true;
-      }
       V kv[2][KSTEPS];
       const int j2[2] = {jm, jp};
 #pragma unroll
@@ -1364,8 +1371,21 @@ __device__ __forceinline__ void gate_tile(
   if (!ok) {
     if (!FB && !in_wg && n_chunks > 0) {
       // The fallback kernel streams again for the queries that need it.
+      // The lanes here that share the first one's list take their places
+      // with one atomic (the order within a list does not matter).
       const int64_t li = rh * kFbBuckets + t / fb.cap;
-      const int e = atomicAdd(fb.count + li, 1);
+      const uint64_t act = __ballot(1);
+      const int lead = __builtin_ffsll(static_cast<long long>(act)) - 1;
+      const bool same = li == __shfl(li, lead);
+      const uint64_t ms = __ballot(same);
+      int e;
+      if (same) {
+        int base = 0;
+        if (lane == lead) base = atomicAdd(fb.count + li, __popcll(ms));
+        e = __shfl(base, lead) + __popcll(ms & ((1ull << lane) - 1));
+      } else {
+        e = atomicAdd(fb.count + li, 1);
+      }
       fb.list[li * fb.cap + e] = make_int2(static_cast<int>(t), __float_as_int(theta));
     } else {
       const int slot = atomicAdd(queue_len, 1);
