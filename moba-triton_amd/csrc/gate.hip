@@ -24,10 +24,11 @@
 //     bound on L (the take-th best of all); theta lies just below the
 //     scores that can round to the key R(bound - w) or above (every
 //     selected key is at least that).
-//   - Decide: |approx - exact| <= E with E = D 2^-22 |q| max|kbar| plus
-//     the denormal terms (twice the D 2^-23 |q| |kbar| that D float32
-//     additions rounding by at most one ulp each can lose), so a score's key (the exact score rounded to
-//     float32 and to the dtype) lies in [R(a - w), R(a + w)], w being E
+//   - Decide: |approx - exact| <= E with E = D 2^-22 |q| max|kbar| (twice
+//     what D float32 additions, each rounding by at most one ulp, can
+//     lose) plus the denormal terms, so a score's key (the exact score
+//     rounded to float32 and to the dtype) lies in [R(a - w), R(a + w)], w
+//     being E
 //     widened by float32 rounding. The candidates (scores >= theta of the
 //     kept groups) are compacted per lane; those with a single possible
 //     key are ranked by it, those straddling a rounding boundary and not
@@ -44,12 +45,16 @@
 //     (row, query head, position bucket).
 //
 // * gate_fallback_kernel: tiles of 128 such queries stream every chunk up
-//   to the tile's horizon, as the second stream above, but the lists rank
-//   by (largest key the score can have, id): everything a full list left
-//   out ranks below its last entry, so many equal keys at the boundary
-//   (keys sharing a large common component) settle by id, as the oracle
-//   breaks ties, instead of going to the queue. The work follows the
-//   number of unsettled queries, not the number of workgroups holding one.
+//   to the tile's horizon, with pass 1's group tracking, but the groups
+//   rank by (largest key any of their scores can have, group id): a group
+//   that left the list then ranks below the one that left last, so many
+//   equal keys at the boundary (keys sharing a large common component)
+//   settle by id, as the oracle breaks ties, instead of going to the
+//   queue; the decision is the first kernel's on those groups. Where the
+//   group ids do not fit the keys' low bits, the tiles stream as the
+//   second stream above instead, into lists ranked by (largest key, id).
+//   The work follows the number of unsettled queries, not the number of
+//   workgroups holding one.
 //
 //   A query that settles nowhere (more straddling candidates than the
 //   buffers hold, constructed ties, inf / NaN input) is queued; it is
@@ -565,7 +570,24 @@ __device__ inline void insert_value(float (&l)[K], float x) {
 // One tile of 32 * WAVES queries of one (row, query head): the queries
 // t0 .. t0 + 32 WAVES - 1 (first kernel, FB false), or entries e0 .. of a
 // fallback list (FB true; `ent` is the list, n_ent its length).
-template <typename T, int D, int M, int K, int CAP, int WAVES, int GB, bool FB>
+// Low mantissa bits that are zero in every float holding a value of T.
+template <typename T> __host__ __device__ constexpr int gate_key_bits() {
+  return Elem<T>::kCode == MOBA_BF16 ? 16 : 13;
+}
+// Whether the group ids and LDS slots of every tile fit those bits: a tile
+// ranks at most n_blocks blocks, in 32-block chunks of 16 / GB groups.
+template <typename T, int K, int GB> static bool gate_keyed_fits(int64_t n_blocks) {
+  const int64_t max_gid = (n_blocks + 31) / 32 * (16 / GB) - 1;
+  int bits = 0;
+  while ((int64_t{1} << bits) <= max_gid) ++bits;
+  const int slot_bits = K == 8 ? 3 : (K == 16 ? 4 : 5);
+  return slot_bits + bits <= gate_key_bits<T>();
+}
+
+// FBM: 0 for the first kernel; for the fallback kernel 1 (groups tracked
+// by (key, id), as long as the group ids fit the keys' low bits) or 2 (every
+// score above the threshold appended to lists).
+template <typename T, int D, int M, int K, int CAP, int WAVES, int GB, int FBM>
 __device__ __forceinline__ void gate_tile(
     const T* __restrict__ q, const T* __restrict__ kbar, int32_t* __restrict__ out,
     const int32_t* __restrict__ cu, int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks,
@@ -574,6 +596,7 @@ __device__ __forceinline__ void gate_tile(
     int64_t rh, int64_t first, const FbLists& fb, const int2* __restrict__ ent, int n_ent) {
   using Ops = MfmaOps<T>;
   using V = typename Ops::vec;
+  constexpr bool FB = FBM != 0;
   constexpr int KSTEPS = D / 16;
   constexpr int KROW = D + 8;                      // staged kbar row stride (elements)
   constexpr int NT = WAVES * 64;
@@ -634,6 +657,7 @@ __device__ __forceinline__ void gate_tile(
     if (lane == 0) atomicMax(&s_hz, m);
     __syncthreads();
     hz = s_hz;
+    if (tid == 0) atomicAdd(queue_len + 1, 1);  // fallback tiles, for tests
   }
   const T* kb = kbar + (r * h_kv + hk) * n_blocks * D;
   const int64_t tok = sp.bos + (live ? t : 0);
@@ -667,7 +691,8 @@ __device__ __forceinline__ void gate_tile(
     }
   qn += __shfl_xor(qn, 32);
   // Accumulation error, plus what flushing denormal operands could drop:
-  // each flushed factor is below kDenorm and its partner below |q| or |kbar|.
+  // each flushed factor is below kDenorm, so the lost products sum to at
+  // most kDenorm (sum |kbar_i| + sum |q_i|) <= kDenorm sqrt(D) (|kbar| + |q|).
   // The products of 16-bit inputs are exact in float32; the D of them reach
   // the result through at most D float32 additions, in any order, each
   // rounding by at most one ulp (2^-23 relative, truncation included) of a
@@ -678,7 +703,7 @@ __device__ __forceinline__ void gate_tile(
   const float knorm = kbar_norm[r * h_kv + hk] * 1.0001f + 1e-30f;
   // The last term covers float32 denormal products or partial sums the
   // matrix core may flush: at most 2^-126 each, D + 1 of them.
-  const float E = qnorm * knorm * (D * 0x1p-22f) + Ops::kDenorm * D * (qnorm + knorm) +
+  const float E = qnorm * knorm * (D * 0x1p-22f) + Ops::kDenorm * sqrtf(D) * (qnorm + knorm) +
                   (D + 1) * 1.2e-38f;
   // E widened by the float32 rounding of a -+ E (2.4e-7 > 2^-22).
   auto widen = [&](float a) { return E * 1.001f + fabsf(a) * 2.4e-7f; };
@@ -796,7 +821,24 @@ __device__ __forceinline__ void gate_tile(
   // Largest key that left the list (or never entered it): every group not
   // in the list has its maximum <= key_hi(ev).
   float ev = -INFINITY;
-  if (!FB && n_chunks > 0) {
+  // The fallback kernel ranks groups by (largest key any of their scores
+  // can have, group id asc): the key R(max + w) as a float, whose low
+  // mantissa bits (16 for bf16, 13 for fp16) are zero, carries in them the
+  // group id (rising for negative keys, falling for positive ones, so that
+  // a lower id ranks first either way) and the LDS slot. Float order is
+  // then exactly that ranking. Where the ids may not fit
+  // (gate_keyed_fits), the host launches FBM = 2, which appends scores.
+  const bool keyed = FBM == 1 && SLOT_BITS + gid_bits <= gate_key_bits<T>();
+  auto keyed_gid = [&](float k) {
+    const uint32_t u = __float_as_uint(k);
+    const int g = static_cast<int>((u & low_mask) >> SLOT_BITS);
+    return (u >> 31) ? g : max_gid - g;
+  };
+  auto keyed_val = [&](float k) {
+    const float f = __uint_as_float(__float_as_uint(k) & ~low_mask);
+    return f <= -3.0e38f ? -INFINITY : f;
+  };
+  if ((!FB || keyed) && n_chunks > 0) {
     const float empty = -INFINITY;
 #pragma unroll
     for (int p = 0; p < K; ++p) {
@@ -813,8 +855,18 @@ __device__ __forceinline__ void gate_tile(
       for (int w = 0; w < GB; ++w) mx = fmaxf(mx, x[w]);
       const float old = gk[K - 1];
       const uint32_t slot = __float_as_uint(old) & (K - 1);
-      const uint32_t low = slot | (static_cast<uint32_t>(gid) << SLOT_BITS);
-      const float key = __uint_as_float((__float_as_uint(mx) & ~low_mask) | low);
+      float key;
+      if constexpr (FB) {
+        // + 0: a key of -0 ranks as +0 (they are equal keys). Clamped to
+        // -+0x1.fep127, whose low 16 bits are zero, so that the low bits
+        // keep it a number (a masked group: "none").
+        const float kr = fminf(fmaxf(Elem<T>::round(mx + widen(mx)) + 0.f, -0x1.fep127f), 0x1.fep127f);
+        const uint32_t g = kr < 0.f ? static_cast<uint32_t>(gid) : static_cast<uint32_t>(max_gid - gid);
+        key = __uint_as_float(__float_as_uint(kr) | (g << SLOT_BITS) | slot);
+      } else {
+        const uint32_t low = slot | (static_cast<uint32_t>(gid) << SLOT_BITS);
+        key = __uint_as_float((__float_as_uint(mx) & ~low_mask) | low);
+      }
       ev = __builtin_amdgcn_fmed3f(ev, old, key);  // ev <= old always
       // The key enters the list iff it beats the last entry, whose slot
       // it takes over.
@@ -848,6 +900,7 @@ __device__ __forceinline__ void gate_tile(
         }
       }
     });
+    if constexpr (!FB) {  // the fallback kernel keeps the first kernel's theta
     float lo[K], plo[K];
 #pragma unroll
     for (int p = 0; p < K; ++p) {
@@ -864,6 +917,7 @@ __device__ __forceinline__ void gate_tile(
       const float kt0 = Elem<T>::round(tau - widen(tau));
       const float mid = 0.5f * (kt0 + key_below<T>(kt0));
       theta = nextafterf(mid - 2.f * widen(mid), -INFINITY);
+    }
     }
   }
   // Collection threshold: a > thr0 is a >= theta.
@@ -1146,16 +1200,17 @@ __device__ __forceinline__ void gate_tile(
 #pragma unroll
     for (int p = 0; p < K; ++p) gu = static_cast<int>(ix >> 2) / (GB / 4) == p ? __float_as_uint(gk[p]) : gu;
     const int hh = static_cast<int>(ix >> 2) % (GB / 4);
-    jx = static_cast<int>((gu & low_mask) >> SLOT_BITS) * 2 * GB + 8 * hh + 4 * half +
-         static_cast<int>(ix & 3);
+    const int gx = FB ? keyed_gid(__uint_as_float(gu)) : static_cast<int>((gu & low_mask) >> SLOT_BITS);
+    jx = gx * 2 * GB + 8 * hh + 4 * half + static_cast<int>(ix & 3);
     const float wd = widen_c(x);
     klo = Elem<T>::round(x - wd);
     khi = Elem<T>::round(x + wd);
   };
-  if (!FB && n_chunks > 0 && live && take > 0) {
+  if ((!FB || keyed) && n_chunks > 0 && live && take > 0) {
 #pragma unroll
     for (int p = 0; p < K; ++p) {
-      if (key_hi(gk[p]) >= theta) {
+      // Keyed: every group in the list (its scores are filtered below).
+      if (FB ? keyed_val(gk[p]) > -INFINITY : key_hi(gk[p]) >= theta) {
         const uint32_t u = __float_as_uint(gk[p]);
 #pragma unroll
         for (int h = 0; h < GB / 4; ++h) {
@@ -1187,9 +1242,9 @@ __device__ __forceinline__ void gate_tile(
         ++ns;
       }
     }
-    rej_mine = fmaxf(key_hi(ev), drop_max);
+    rej_mine = FB ? drop_max : fmaxf(key_hi(ev), drop_max);
   }
-  if constexpr (!FB) {
+  if (!FB || keyed) {
     float pv[TS];
     int pi[TS];
 #pragma unroll
@@ -1255,12 +1310,33 @@ __device__ __forceinline__ void gate_tile(
     }
     const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
     const float U = fmaxf(rej, theta);
-    if (ok && take > 0 && live && U > -INFINITY) {
+    if (!FB && ok && take > 0 && live && U > -INFINITY) {
       const float Uk = Elem<T>::round(U + widen(U));
       float kt = -INFINITY;
 #pragma unroll
       for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
       if (!(kt > Uk)) ok = false;
+    }
+    if (FB && ok && take > 0 && live) {
+      // Scores below theta and candidates that found the buffer full have
+      // keys at most R(U + w(U)). A group that left a lane's list ranks at
+      // or below that lane's ev by (key, group id): its scores' keys are at
+      // most ev's key, and where equal to it, its blocks have ids at or
+      // above ev's group's lowest block.
+      float kt = -INFINITY;
+      int it = 0x7fffffff;
+#pragma unroll
+      for (int p = 0; p < TS; ++p) {
+        kt = p == take - 1 ? fv[p] : kt;
+        it = p == take - 1 ? fi[p] : it;
+      }
+      if (U > -INFINITY && !(kt > Elem<T>::round(U + widen(U)))) ok = false;
+      const float evk = keyed_val(ev);
+      const int ev_lo = evk > -INFINITY ? keyed_gid(ev) * 2 * GB + 4 * half : 0x7fffffff;
+      const bool mine = !(evk > kt) && !(evk == kt && ev_lo <= it);
+      // Both lanes of the pair take part in the shuffle (no short circuit).
+      const bool partner = __shfl_xor(mine ? 1 : 0, 32) != 0;
+      if (!(mine && partner)) ok = false;
     }
   }
 
@@ -1280,8 +1356,8 @@ __device__ __forceinline__ void gate_tile(
   const int n_uns =
       FB ? 0 : __syncthreads_count((live && half == 0 && !ok && n_chunks > 0) ? 1 : 0);
   const bool in_wg = !FB && n_uns > 0 && n_uns <= kInWg;
-  if ((FB || in_wg) && n_chunks > 0) {
-    if (FB && tid == 0) atomicAdd(queue_len + 1, 1);  // fallback tiles, for tests
+  if (FBM == 1 && !keyed) ok = false;  // not launched so: a guard
+  if ((FBM == 2 || in_wg) && n_chunks > 0) {
     if (in_wg) reload_q(bq);
     clear_lists();
     float thr = thr0;
@@ -1416,7 +1492,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                  int64_t rows_per_seq, FbLists fb) {
   const int64_t n_tiles = (rows_per_seq + 32 * WAVES - 1) / (32 * WAVES);
   const int64_t tile = n_tiles - 1 - blockIdx.x;
-  gate_tile<T, D, M, K, CAP, WAVES, GB, false>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
+  gate_tile<T, D, M, K, CAP, WAVES, GB, 0>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
                                                take, cur, slots, kbar_norm, queue, queue_len,
                                                rows_per_seq, blockIdx.y, tile * 32 * WAVES, fb,
                                                nullptr, 0);
@@ -1426,7 +1502,7 @@ gate_mfma_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 // bucket) list per grid row, 32 * WAVES per tile, the workgroups of a row
 // striding over its tiles. The work is proportional to the unsettled
 // queries, not to the tiles that hold one.
-template <typename T, int D, int M, int K, int CAP, int WAVES, int GB>
+template <typename T, int D, int M, int K, int CAP, int WAVES, int GB, int FBM>
 __global__ void __launch_bounds__(WAVES * 64, M <= 12 ? (D == 64 ? 3 : 2) : 1)
 gate_fallback_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                      int32_t* __restrict__ out, const int32_t* __restrict__ cu,
@@ -1434,13 +1510,16 @@ gate_fallback_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                      int take, int cur, int slots, const float* __restrict__ kbar_norm,
                      int64_t* __restrict__ queue, int* __restrict__ queue_len,
                      int64_t rows_per_seq, FbLists fb) {
-  const int64_t li = blockIdx.y;
+  // Grid rows run the last position bucket (the longest streams) of every
+  // (row, query head) first, down to bucket 0, so the long tiles start first.
+  const int64_t n_rh = gridDim.y / kFbBuckets;
+  const int64_t li = (blockIdx.y % n_rh) * kFbBuckets + (kFbBuckets - 1 - blockIdx.y / n_rh);
   const int n = fb.count[li];
   const int2* ent = fb.list + li * fb.cap;
   for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * 32 * WAVES; e0 < n;
        e0 += static_cast<int64_t>(gridDim.x) * 32 * WAVES) {
     __syncthreads();  // the previous tile's LDS reads are done
-    gate_tile<T, D, M, K, CAP, WAVES, GB, true>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
+    gate_tile<T, D, M, K, CAP, WAVES, GB, FBM>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
                                                 take, cur, slots, kbar_norm, queue, queue_len,
                                                 rows_per_seq, li / kFbBuckets, e0, fb, ent, n);
   }
@@ -1583,11 +1662,17 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
   // workgroup past its list's length exits at once.
   const int64_t per_list = cdiv(ws.fb_cap, 32 * WAVES) < 32 ? cdiv(ws.fb_cap, 32 * WAVES) : 32;
   dim3 fgrid(static_cast<unsigned>(per_list), static_cast<unsigned>(g.rows * g.h_q * kFbBuckets));
-  hipLaunchKernelGGL((gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB>), fgrid, dim3(64 * WAVES),
-                     0, st, static_cast<const T*>(q), static_cast<const T*>(kbar), out, cu,
-                     g.seq_len, g.h_q, g.h_kv, g.n_blocks, static_cast<int>(g.block_size),
-                     take, cur, static_cast<int>(g.slots), ws.kbar_norm, ws.queue,
-                     ws.counter, g.rows_per_seq, fb);
+  auto fallback = [&](auto kern) {
+    hipLaunchKernelGGL(kern, fgrid, dim3(64 * WAVES), 0, st, static_cast<const T*>(q),
+                       static_cast<const T*>(kbar), out, cu, g.seq_len, g.h_q, g.h_kv,
+                       g.n_blocks, static_cast<int>(g.block_size), take, cur,
+                       static_cast<int>(g.slots), ws.kbar_norm, ws.queue, ws.counter,
+                       g.rows_per_seq, fb);
+  };
+  if (gate_keyed_fits<T, K, GB>(g.n_blocks))
+    fallback(gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB, 1>);
+  else
+    fallback(gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB, 2>);
   return check_launch("moba_gate (fallback)");
 }
 

@@ -229,9 +229,11 @@ def test_gate_fallback_settles_heavy_ties_exactly(device, dtype):
     cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
     shape = (1, 8192, 2, 64)
     g = torch.Generator().manual_seed(39)
-    scale = 1.0 if dtype is torch.bfloat16 else 0.25
+    # float16 keys are finer (10 mantissa bits), so its offset is larger:
+    # scores near 800, where a float16 step (0.5) is twice their spread.
+    scale, offset = (1.0, 8.0) if dtype is torch.bfloat16 else (0.5, 48.0)
     q = (torch.randn(shape, generator=g) * scale).to(dtype).to(device)
-    k = ((8.0 * torch.randn((1, 1, 2, 64), generator=g) + torch.randn(shape, generator=g))
+    k = ((offset * torch.randn((1, 1, 2, 64), generator=g) + torch.randn(shape, generator=g))
          * scale).to(dtype).to(device)
     kbar = pool_blocks(k, cfg)
     b, s, h, d = q.shape
