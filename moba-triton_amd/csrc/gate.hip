@@ -37,12 +37,10 @@
 //     stands when everything left out (groups that left the list, scores
 //     below theta, candidates beyond the buffers) has a key bound strictly
 //     below the take-th selected key.
-//   - A workgroup with a few unsettled queries (at most 4) streams every
-//     chunk a second time: each score above the lane's threshold is
-//     appended to a per-lane LDS buffer, folded into a list of the M best
-//     when it may overflow, and the decision runs on those lists. A
-//     workgroup with more hands them, with their theta, to lists per
-//     (row, query head, position bucket).
+//   - Unsettled queries go, with their theta, to lists per (row, query
+//     head, position bucket) for the fallback kernel. (A second stream in
+//     the workgroup itself for up to 4 of them, the earlier design, cost
+//     offset keys 0.2 ms for 0.02 ms on i.i.d. keys.)
 //
 // * gate_fallback_kernel: tiles of 128 such queries stream every chunk up
 //   to the tile's horizon, with pass 1's group tracking, but the groups
@@ -51,8 +49,9 @@
 //   equal keys at the boundary (keys sharing a large common component)
 //   settle by id, as the oracle breaks ties, instead of going to the
 //   queue; the decision is the first kernel's on those groups. Where the
-//   group ids do not fit the keys' low bits, the tiles stream as the
-//   second stream above instead, into lists ranked by (largest key, id).
+//   group ids do not fit the keys' low bits, the tiles append every score
+//   above the lane's threshold to a per-lane LDS buffer instead, folded
+//   into lists of the M best by (largest key, id).
 //   The work follows the number of unsettled queries, not the number of
 //   workgroups holding one.
 //
@@ -219,18 +218,20 @@ __device__ inline bool ranks_before(float s, int j, float v, int i) {
 
 // Inserts (s, j) into a list sorted by (score desc, id asc); the last entry
 // falls off. Entries with score -inf / NaN never enter.
+// Branch-free: every step selects, so a wave never splits over the list.
 template <int M>
 __device__ inline void insert_exact(float (&val)[M], int (&idx)[M], float s, int j) {
   bool carry = false;
 #pragma unroll
   for (int p = 0; p < M; ++p) {
-    bool take = carry || ranks_before(s, j, val[p], idx[p]);
-    if (take) {
-      float tv = val[p]; int ti = idx[p];
-      val[p] = s; idx[p] = j;
-      s = tv; j = ti;
-      carry = true;
-    }
+    const bool take = carry || ranks_before(s, j, val[p], idx[p]);
+    const float tv = val[p];
+    const int ti = idx[p];
+    val[p] = take ? s : tv;
+    idx[p] = take ? j : ti;
+    s = take ? tv : s;
+    j = take ? ti : j;
+    carry = take;
   }
 }
 
@@ -261,22 +262,6 @@ __device__ inline void merge_top(float (&val)[M], int (&idx)[M], const float (&p
         val[p + st] = tv;
         idx[p + st] = ti;
       }
-}
-
-// Branch-free insertion into a list sorted by value only (approximate scores;
-// ties among them are settled later by the exact rescoring).
-template <int M>
-__device__ inline void insert_approx(float (&val)[M], int (&idx)[M], float s, int j) {
-#pragma unroll
-  for (int p = 0; p < M; ++p) {
-    const bool gt = s > val[p];
-    const float nv = gt ? s : val[p];
-    const int ni = gt ? j : idx[p];
-    s = gt ? val[p] : s;
-    j = gt ? idx[p] : j;
-    val[p] = nv;
-    idx[p] = ni;
-  }
 }
 
 // k-th largest (1-based, k <= M) of the union of two lists sorted in
@@ -957,94 +942,6 @@ __device__ __forceinline__ void gate_tile(
   float fv[TS];
   int fi[TS];
   uint32_t* su = reinterpret_cast<uint32_t*>(sv);
-  // The first kernel's own fallback ranks its lists by approximate score
-  // alone: what they left out scores at most rej, the larger of the two
-  // lanes' rej_mine, and its key is at most R(U + w(U)), U = max(theta, rej).
-  auto decide_value = [&]() -> bool {
-    const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
-    float pv[M];
-    int pi[M];
-#pragma unroll
-    for (int p = 0; p < M; ++p) {
-      pv[p] = __shfl_xor(lv[p], 32);
-      pi[p] = __shfl_xor(li[p], 32);
-    }
-    // L: the take-th approximate score of the union. At least `take` listed
-    // candidates have keys >= Lk; one whose key interval ends below Lk is
-    // outranked by all of them.
-    const float L = take > 0 ? kth_of_union<M>(lv, pv, take) : -INFINITY;
-    const float Lk = L > -INFINITY ? Elem<T>::round(L - widen(L)) : -INFINITY;
-    // q or kbar carries inf / NaN, or a score could round to an infinite key.
-    bool ok = !(take > 0) || (qnorm * knorm < Ops::kMaxFinite);
-#pragma unroll
-    for (int p = 0; p < TS; ++p) { fv[p] = -INFINITY; fi[p] = 0x7fffffff; }
-    // The candidates that can still rank in the top `take`, with exact keys,
-    // in (key desc, id asc) order. Both lanes walk the union in the same
-    // order (half 0's list first) and reach identical lists; uncertain ids
-    // wait in the lane's candidate buffer and are rescored (float64) by the
-    // two lanes together, each forming the partial dot over the features it
-    // holds.
-    if (ok && take > 0 && live) {
-      int nu = 0;
-      auto visit = [&](float x, int j) {
-        if (!(x > -INFINITY)) return;
-        const float w = widen(x);
-        const float khi = Elem<T>::round(x + w);
-        if (khi < Lk) return;
-        const float klo = Elem<T>::round(x - w);
-        if (klo == khi) {
-          insert_exact<TS>(fv, fi, klo, j);
-        } else {
-          if (nu < CAP) su[nu * 64] = static_cast<uint32_t>(j);
-          ++nu;
-        }
-      };
-#pragma unroll
-      for (int p = 0; p < M; ++p) visit(half == 0 ? lv[p] : pv[p], half == 0 ? li[p] : pi[p]);
-#pragma unroll
-      for (int p = 0; p < M; ++p) visit(half == 0 ? pv[p] : lv[p], half == 0 ? pi[p] : li[p]);
-      if (nu > CAP) ok = false;  // more straddling candidates than the buffer holds
-      constexpr int R = 2;
-      V qv[KSTEPS];
-      if (nu > 0) reload_q(qv);
-#pragma unroll 1
-      for (int u0 = 0; ok && u0 < nu; u0 += R) {
-        int jr[R];
-        V kv[R][KSTEPS];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          jr[r] = u0 + r < nu ? static_cast<int>(su[(u0 + r) * 64]) : 0;
-          jr[r] = jr[r] < hz ? jr[r] : 0;  // ids come from this lane's lists; a guard
-          const T* krow = kb + static_cast<int64_t>(jr[r]) * D + 8 * half;
-#pragma unroll
-          for (int c = 0; c < KSTEPS; ++c) kv[r][c] = load_vec16<V>(krow + 16 * c);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          double part = 0.0;
-#pragma unroll
-          for (int c = 0; c < KSTEPS; ++c)
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              part += static_cast<double>(static_cast<float>(qv[c][i])) *
-                      static_cast<double>(static_cast<float>(kv[r][c][i]));
-          part += __shfl_xor(part, 32);
-          const float sc = Elem<T>::round(static_cast<float>(part));
-          if (u0 + r < nu && sc > -INFINITY) insert_exact<TS>(fv, fi, sc, jr[r]);
-        }
-      }
-      // Candidates outside the lists must rank below the take-th selected.
-      const float U = fmaxf(rej, theta);
-      if (U > -INFINITY) {
-        const float Uk = Elem<T>::round(U + widen(U));
-        float kt = -INFINITY;
-#pragma unroll
-        for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
-        if (!(kt > Uk)) ok = false;
-      }
-    }
-    return ok;
-  };
   // The fallback kernel's lists rank by (largest key, id), so equal keys at
   // the boundary settle by id.
   auto decide_keyed = [&]() -> bool {
@@ -1340,35 +1237,21 @@ __device__ __forceinline__ void gate_tile(
     }
   }
 
-  // --- Fallback: pass 2 streams every chunk again for queries the decision
-  // above left unsettled. A workgroup of the first kernel with at most
-  // kInWg of them streams again itself (for all its queries); one with
-  // more hands them to gate_fallback_kernel, whose tiles hold only such
-  // queries (FB). Each score above the lane's threshold (rare: theta sits
-  // about one key below L) is appended, with its block id, to the lane's
-  // LDS buffer; a buffer that may overflow on the next chunk is folded
-  // into the lane's list of its M best, and the threshold rises to the
-  // last entry's score.
-  // At head_dim 128 the first kernel's registers cannot hold the second
-  // stream as well (it spilled 94 dwords and ran 12% slower at config 4),
-  // so every unsettled query goes to the fallback kernel.
-  constexpr int kInWg = D == 64 ? 4 : 0;
-  const int n_uns =
-      FB ? 0 : __syncthreads_count((live && half == 0 && !ok && n_chunks > 0) ? 1 : 0);
-  const bool in_wg = !FB && n_uns > 0 && n_uns <= kInWg;
+  // --- Appending fallback (FBM 2: group ids too wide for keyed groups):
+  // stream every chunk again. Each score above the lane's threshold (rare:
+  // theta sits about one key below L) is appended, with its block id, to
+  // the lane's LDS buffer; a buffer that may overflow on the next chunk is
+  // folded into the lane's list of its M best by (largest key, id), and the
+  // threshold rises to the last entry's score.
   if (FBM == 1 && !keyed) ok = false;  // not launched so: a guard
-  if ((FBM == 2 || in_wg) && n_chunks > 0) {
-    if (in_wg) reload_q(bq);
+  if (FBM == 2 && n_chunks > 0) {
     clear_lists();
     float thr = thr0;
     int cnt = 0;
     auto fold = [&]() {
       for (int e = 0; e < cnt; ++e) {
         const float x = sv[e * 64];
-        if constexpr (FB)
-          insert_keyed<M>(lk, lv, li, Elem<T>::round(x + widen(x)), x, si[e * 64]);
-        else
-          insert_approx<M>(lv, li, x, si[e * 64]);
+        insert_keyed<M>(lk, lv, li, Elem<T>::round(x + widen(x)), x, si[e * 64]);
       }
       cnt = 0;
       // A full list takes a later score only if it can beat the last entry.
@@ -1431,21 +1314,13 @@ __device__ __forceinline__ void gate_tile(
       if (__any(cnt > CAP - 16)) fold();
     });
     fold();
-    if constexpr (FB) {
-      ok = decide_keyed();
-    } else {
-      int n_in_list = 0;
-#pragma unroll
-      for (int p = 0; p < M; ++p) n_in_list += lv[p] > -INFINITY ? 1 : 0;
-      rej_mine = (n_in_list == M) ? lv[M - 1] : -INFINITY;
-      ok = decide_value();
-    }
+    ok = decide_keyed();
   }
 
   if (!live || half != 0) return;
   const int64_t qid = hm_query(packed, r, hq, h_q, S, tok, t);
   if (!ok) {
-    if (!FB && !in_wg && n_chunks > 0) {
+    if (!FB && n_chunks > 0) {
       // The fallback kernel streams again for the queries that need it.
       // The lanes here that share the first one's list take their places
       // with one atomic (the order within a list does not matter).
