@@ -570,8 +570,10 @@ template <typename T, int K, int GB> static bool gate_keyed_fits(int64_t n_block
 }
 
 // FBM: 0 for the first kernel; for the fallback kernel 1 (groups tracked
-// by (key, id), as long as the group ids fit the keys' low bits) or 2 (every
-// score above the threshold appended to lists).
+// by (key, id), as long as the group ids fit the keys' low bits), 2 (every
+// score above the threshold appended to lists) or 3 (as 1, for a tile of at
+// most 32 queries: every wave takes the same queries and a quarter of the
+// chunks, and wave 0 merges the four lists and decides).
 template <typename T, int D, int M, int K, int CAP, int WAVES, int GB, int FBM>
 __device__ __forceinline__ void gate_tile(
     const T* __restrict__ q, const T* __restrict__ kbar, int32_t* __restrict__ out,
@@ -582,6 +584,7 @@ __device__ __forceinline__ void gate_tile(
   using Ops = MfmaOps<T>;
   using V = typename Ops::vec;
   constexpr bool FB = FBM != 0;
+  constexpr bool SPLIT = FBM == 3;
   constexpr int KSTEPS = D / 16;
   constexpr int KROW = D + 8;                      // staged kbar row stride (elements)
   constexpr int NT = WAVES * 64;
@@ -628,7 +631,7 @@ __device__ __forceinline__ void gate_tile(
     // Queries of one list in no particular order: the horizon is the
     // largest own block of the tile.
     __shared__ int s_hz;
-    const int64_t e = first + wave * 32 + col;
+    const int64_t e = first + (SPLIT ? 0 : wave * 32) + col;
     live = e < n_ent;
     const int2 en = live ? ent[e] : make_int2(0, 0);
     t = en.x;
@@ -779,6 +782,36 @@ __device__ __forceinline__ void gate_tile(
       step(st + 1, kr0, kr1);
     }
   };
+  // SPLIT: wave w scores chunks w, w + WAVES, ... of the same queries, its
+  // A operands loaded straight from kbar (no staging, no barriers), three
+  // chunks in flight.
+  auto split_stream = [&](auto&& body) {
+    auto aload = [&](V (&dst)[KSTEPS], int ch) {
+      const int blk = min(32 * ch + col, hz - 1);
+      const T* row = kb + static_cast<int64_t>(blk) * D + 8 * half;
+#pragma unroll
+      for (int c = 0; c < KSTEPS; ++c) dst[c] = load_vec16<V>(row + 16 * c);
+    };
+    // step(c): score chunk c from `cur`, after requesting chunk c + 2 WAVES
+    // into `freed` (the buffer chunk c - WAVES was scored from).
+    // Inlined, so that the three buffers stay in registers.
+    auto step = [&](int c, const V (&cur)[KSTEPS], V (&freed)[KSTEPS]) __attribute__((always_inline)) {
+      if (c >= n_chunks) return;
+      if (c + 2 * WAVES < n_chunks) aload(freed, c + 2 * WAVES);
+      floatx16_t acc = {};
+#pragma unroll
+      for (int k = 0; k < KSTEPS; ++k) acc = Ops::mfma(cur[k], bq[k], acc);
+      body(c, acc, c * 32 + 32 <= own_min);
+    };
+    V a0[KSTEPS], a1[KSTEPS], a2[KSTEPS];
+    if (wave < n_chunks) aload(a0, wave);
+    if (wave + WAVES < n_chunks) aload(a1, wave + WAVES);
+    for (int c = wave; c < n_chunks; c += 3 * WAVES) {
+      step(c, a0, a2);
+      step(c + WAVES, a1, a0);
+      step(c + 2 * WAVES, a2, a1);
+    }
+  };
   // Group keys. A group is four consecutive blocks of one lane (lane half h
   // holds the groups with (block >> 2) & 1 == h), numbered gid = block >> 3
   // within the lane. A key is the group's maximum score with its low
@@ -813,7 +846,7 @@ __device__ __forceinline__ void gate_tile(
   // a lower id ranks first either way) and the LDS slot. Float order is
   // then exactly that ranking. Where the ids may not fit
   // (gate_keyed_fits), the host launches FBM = 2, which appends scores.
-  const bool keyed = FBM == 1 && SLOT_BITS + gid_bits <= gate_key_bits<T>();
+  const bool keyed = (FBM == 1 || SPLIT) && SLOT_BITS + gid_bits <= gate_key_bits<T>();
   auto keyed_gid = [&](float k) {
     const uint32_t u = __float_as_uint(k);
     const int g = static_cast<int>((u & low_mask) >> SLOT_BITS);
@@ -863,7 +896,7 @@ __device__ __forceinline__ void gate_tile(
       }
       insert_value<K>(gk, key);
     };
-    stream_chunks([&](int ch, const floatx16_t& acc, bool full) {
+    auto chunk = [&](int ch, const floatx16_t& acc, bool full) {
       if (full) {
 #pragma unroll
         for (int g = 0; g < GPC; ++g) {
@@ -884,7 +917,56 @@ __device__ __forceinline__ void gate_tile(
           track(x, gid);
         }
       }
-    });
+    };
+    if constexpr (SPLIT) {
+      split_stream(chunk);
+      // Wave 0 takes the K best groups of the four waves' lists by (key,
+      // id), their records moved to its own slots 0 .. K - 1; every group
+      // left out ranks at or below the largest key that left a list (ev).
+      float* mk = reinterpret_cast<float*>(&s_kb[0][0]);  // [WAVES][K + 1][64]
+      static_assert(WAVES * (K + 1) * 64 * 4 <= sizeof(s_kb), "merge area");
+#pragma unroll
+      for (int p = 0; p < K; ++p) mk[(wave * (K + 1) + p) * 64 + lane] = gk[p];
+      mk[(wave * (K + 1) + K) * 64 + lane] = ev;
+      __syncthreads();
+      if (wave != 0) return;
+      int src[K];  // record of each entry: wave * K + slot
+#pragma unroll
+      for (int p = 0; p < K; ++p) src[p] = static_cast<int>(__float_as_uint(gk[p]) & (K - 1));
+      for (int w = 1; w < WAVES; ++w) {
+        ev = fmaxf(ev, mk[(w * (K + 1) + K) * 64 + lane]);
+#pragma unroll
+        for (int p = 0; p < K; ++p) {
+          float k = mk[(w * (K + 1) + p) * 64 + lane];
+          int si = w * K + static_cast<int>(__float_as_uint(k) & (K - 1));
+          ev = fmaxf(ev, fminf(gk[K - 1], k));  // what this insertion drops
+#pragma unroll
+          for (int u = 0; u < K; ++u) {
+            const bool gt = k > gk[u];
+            const float nk = gt ? k : gk[u];
+            const int ns = gt ? si : src[u];
+            k = gt ? gk[u] : k;
+            si = gt ? src[u] : si;
+            gk[u] = nk;
+            src[u] = ns;
+          }
+        }
+      }
+      // (u32x4, not float4: an array of HIP's float4 struct stays in memory.)
+      static_assert(GB == 4, "one 16-byte record per group");
+      u32x4 rec[K];
+      const u32x4* recs = reinterpret_cast<const u32x4*>(&s_wave[0][0]) + lane;
+      constexpr int kWaveRecs = sizeof(s_wave[0]) / 16;
+#pragma unroll
+      for (int p = 0; p < K; ++p) rec[p] = recs[(src[p] / K) * kWaveRecs + (src[p] % K) * 64];
+#pragma unroll
+      for (int p = 0; p < K; ++p) {
+        reinterpret_cast<u32x4*>(srec)[p * 64] = rec[p];
+        gk[p] = __uint_as_float((__float_as_uint(gk[p]) & ~static_cast<uint32_t>(K - 1)) | p);
+      }
+    } else {
+      stream_chunks(chunk);
+    }
     if constexpr (!FB) {  // the fallback kernel keeps the first kernel's theta
     float lo[K], plo[K];
 #pragma unroll
@@ -1243,7 +1325,7 @@ __device__ __forceinline__ void gate_tile(
   // the lane's LDS buffer; a buffer that may overflow on the next chunk is
   // folded into the lane's list of its M best by (largest key, id), and the
   // threshold rises to the last entry's score.
-  if (FBM == 1 && !keyed) ok = false;  // not launched so: a guard
+  if ((FBM == 1 || SPLIT) && !keyed) ok = false;  // not launched so: a guard
   if (FBM == 2 && n_chunks > 0) {
     clear_lists();
     float thr = thr0;
@@ -1384,15 +1466,30 @@ gate_fallback_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                      int64_t S, int64_t h_q, int64_t h_kv, int64_t n_blocks, int bs,
                      int take, int cur, int slots, const float* __restrict__ kbar_norm,
                      int64_t* __restrict__ queue, int* __restrict__ queue_len,
-                     int64_t rows_per_seq, FbLists fb) {
+                     int64_t rows_per_seq, FbLists fb, int split_tail) {
   // Grid rows run the last position bucket (the longest streams) of every
   // (row, query head) first, down to bucket 0, so the long tiles start first.
   const int64_t n_rh = gridDim.y / kFbBuckets;
   const int64_t li = (blockIdx.y % n_rh) * kFbBuckets + (kFbBuckets - 1 - blockIdx.y / n_rh);
   const int n = fb.count[li];
   const int2* ent = fb.list + li * fb.cap;
-  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * 32 * WAVES; e0 < n;
-       e0 += static_cast<int64_t>(gridDim.x) * 32 * WAVES) {
+  // A last tile of at most 32 queries goes to the split kernel (FBM 3), when
+  // it runs: its four waves share the chunks instead of one wave holding
+  // every query.
+  constexpr int TQ = 32 * WAVES;
+  const int tail = n % TQ;
+  const bool split = split_tail && tail > 0 && tail <= 32;
+  if constexpr (FBM == 3) {
+    if (!split || blockIdx.x != 0) return;  // uniform
+    gate_tile<T, D, M, K, CAP, WAVES, GB, FBM>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
+                                                take, cur, slots, kbar_norm, queue, queue_len,
+                                                rows_per_seq, li / kFbBuckets, n - tail, fb, ent,
+                                                n);
+    return;
+  }
+  const int n_full = split ? n - tail : n;
+  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * TQ; e0 < n_full;
+       e0 += static_cast<int64_t>(gridDim.x) * TQ) {
     __syncthreads();  // the previous tile's LDS reads are done
     gate_tile<T, D, M, K, CAP, WAVES, GB, FBM>(q, kbar, out, cu, S, h_q, h_kv, n_blocks, bs,
                                                 take, cur, slots, kbar_norm, queue, queue_len,
@@ -1537,17 +1634,24 @@ static int launch_mfma(const void* q, const void* kbar, int32_t* out, const int3
   // workgroup past its list's length exits at once.
   const int64_t per_list = cdiv(ws.fb_cap, 32 * WAVES) < 32 ? cdiv(ws.fb_cap, 32 * WAVES) : 32;
   dim3 fgrid(static_cast<unsigned>(per_list), static_cast<unsigned>(g.rows * g.h_q * kFbBuckets));
+  // Keyed groups: lists' last tiles of at most 32 queries (all of them on
+  // i.i.d. keys, where a few queries per list are unsettled) go to the
+  // split kernel, one workgroup per list.
+  const int split_tail = gate_keyed_fits<T, K, GB>(g.n_blocks) ? 1 : 0;
   auto fallback = [&](auto kern) {
     hipLaunchKernelGGL(kern, fgrid, dim3(64 * WAVES), 0, st, static_cast<const T*>(q),
                        static_cast<const T*>(kbar), out, cu, g.seq_len, g.h_q, g.h_kv,
                        g.n_blocks, static_cast<int>(g.block_size), take, cur,
                        static_cast<int>(g.slots), ws.kbar_norm, ws.queue, ws.counter,
-                       g.rows_per_seq, fb);
+                       g.rows_per_seq, fb, split_tail);
   };
-  if (gate_keyed_fits<T, K, GB>(g.n_blocks))
+  if (split_tail) {
     fallback(gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB, 1>);
-  else
+    fgrid.x = 1;
+    fallback(gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB, 3>);
+  } else {
     fallback(gate_fallback_kernel<T, D, M, K, CAP, WAVES, GB, 2>);
+  }
   return check_launch("moba_gate (fallback)");
 }
 
