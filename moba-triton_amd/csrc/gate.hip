@@ -543,13 +543,23 @@ __device__ inline V load_vec16(const void* p) {
   return __builtin_bit_cast(V, u);
 }
 
+// +inf in a register the compiler cannot see through: a med3 against it
+// stays one instruction (against the constant the compiler turns it into a
+// max that canonicalises both operands first, three instructions).
+__device__ inline float opaque_inf() {
+  float inf = INFINITY;
+  asm volatile("" : "+v"(inf));
+  return inf;
+}
+
 // Inserts x into a list of values sorted descending; the smallest falls off.
-// New entry p is the median of old entries p - 1, p and x.
+// New entry p is the median of old entries p - 1, p and x; `inf` is +inf
+// (from opaque_inf, made once outside the caller's loop).
 template <int K>
-__device__ inline void insert_value(float (&l)[K], float x) {
+__device__ inline void insert_value(float (&l)[K], float x, float inf) {
 #pragma unroll
   for (int p = K - 1; p > 0; --p) l[p] = __builtin_amdgcn_fmed3f(l[p - 1], l[p], x);
-  l[0] = __builtin_amdgcn_fmed3f(l[0], x, INFINITY);  // max, without canonicalising
+  l[0] = __builtin_amdgcn_fmed3f(l[0], x, inf);  // max, without canonicalising
 }
 
 // One tile of 32 * WAVES queries of one (row, query head): the queries
@@ -866,6 +876,7 @@ __device__ __forceinline__ void gate_tile(
         srec[(p * (GB / 4) + h) * 64] = make_float4(empty, empty, empty, empty);
     }
     // Element w of group gid scores block gid 2GB + 8 (w / 4) + 4 half + w % 4.
+    const float pinf = opaque_inf();
     auto track = [&](const float (&x)[GB], int gid) {
       // Clamped to -FLT_MAX so that replacing low bits keeps it a number.
       float mx = -3.4028235e38f;
@@ -894,7 +905,7 @@ __device__ __forceinline__ void gate_tile(
           srec[(slot * (GB / 4) + h) * 64] =
               make_float4(x[4 * h], x[4 * h + 1], x[4 * h + 2], x[4 * h + 3]);
       }
-      insert_value<K>(gk, key);
+      insert_value<K>(gk, key, pinf);
     };
     auto chunk = [&](int ch, const floatx16_t& acc, bool full) {
       if (full) {
@@ -1055,10 +1066,11 @@ __device__ __forceinline__ void gate_tile(
 #pragma unroll
       for (int p = 0; p < TS; ++p) kl[p] = -INFINITY;
       auto lower = [&](float x) { return x > -INFINITY ? Elem<T>::round(x - widen(x)) : -INFINITY; };
+      const float kinf = opaque_inf();
 #pragma unroll
-      for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? lv[p] : pv[p]));
+      for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? lv[p] : pv[p]), kinf);
 #pragma unroll
-      for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? pv[p] : lv[p]));
+      for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? pv[p] : lv[p]), kinf);
       float Lk = -INFINITY;
 #pragma unroll
       for (int p = 0; p < TS; ++p) Lk = p == take - 1 ? kl[p] : Lk;
@@ -1209,11 +1221,12 @@ __device__ __forceinline__ void gate_tile(
     // Straddlers move to the front of the buffer (in place: the write
     // index never passes the read index); ns of them.
     const int ce = min(cn, C);
+    const float kinf = opaque_inf();
     for (int e = 0; e < ce; ++e) {
       float x, klo, khi;
       int jx;
       cand(e, x, jx, klo, khi);
-      insert_value<TS>(kl, klo);
+      insert_value<TS>(kl, klo, kinf);
       if (klo == khi) {
         insert_exact<TS>(fv, fi, klo, jx);
       } else {
