@@ -1174,6 +1174,8 @@ __device__ __forceinline__ void gate_tile(
   constexpr int C = CB < 24 ? CB : 24;
   static_assert(C >= 4, "candidate buffer");
   float* cbuf = reinterpret_cast<float*>(&s_kb[0][0]) + wave * (C + 1) * 64 + lane;
+  // The kept groups' keys, stored over the records once these are compacted.
+  float* gks = reinterpret_cast<float*>(&s_wave[wave][0]) + lane;
   uint32_t* su_c = reinterpret_cast<uint32_t*>(cbuf);
   auto widen_c = [&](float a) { return widen(a) + fabsf(a) * ldexpf(1.f, IB - 22); };
   int cn = 0;
@@ -1186,10 +1188,9 @@ __device__ __forceinline__ void gate_tile(
   auto cand = [&](int e, float& x, int& jx, float& klo, float& khi) {
     x = cbuf[e * 64];
     const uint32_t ix = __float_as_uint(x) & IMASK;
-    // Block id from the kept group's key: p selects among the registers.
-    uint32_t gu = 0;
-#pragma unroll
-    for (int p = 0; p < K; ++p) gu = static_cast<int>(ix >> 2) / (GB / 4) == p ? __float_as_uint(gk[p]) : gu;
+    // Block id from the kept group's key, read back from LDS (one read in
+    // place of a select over the K registers).
+    const uint32_t gu = __float_as_uint(gks[((ix >> 2) / (GB / 4)) * 64]);
     const int hh = static_cast<int>(ix >> 2) % (GB / 4);
     const int gx = FB ? keyed_gid(__uint_as_float(gu)) : static_cast<int>((gu & low_mask) >> SLOT_BITS);
     jx = gx * 2 * GB + 8 * hh + 4 * half + static_cast<int>(ix & 3);
@@ -1218,6 +1219,8 @@ __device__ __forceinline__ void gate_tile(
         }
       }
     }
+#pragma unroll
+    for (int p = 0; p < K; ++p) gks[p * 64] = gk[p];
     // Straddlers move to the front of the buffer (in place: the write
     // index never passes the read index); ns of them.
     const int ce = min(cn, C);
