@@ -79,6 +79,17 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte chunk
 // Unsettled queries of gate_mfma_kernel wait for gate_fallback_kernel in
 // lists per (row, query head, position bucket): (t, theta bits) pairs, cap
 // entries per list (a bucket holds cap consecutive positions).
+// A float rounded to T, to nearest even: bf16 takes the hardware conversion
+// (v_cvt_pk_bf16_f32: round to nearest even, denormals kept, NaN quiet;
+// equal to float_to_bf16 on all 2^32 inputs, in two instructions). Exact
+// scores, computed in double, round through Elem<T>::round instead: given
+// the cast of a double to float and then to __bf16, the compiler rounds the
+// double to bf16 once, which is not the key (float first, then bf16).
+template <typename T> __device__ inline float key_round(float v) { return Elem<T>::round(v); }
+template <> __device__ inline float key_round<bf16_t>(float v) {
+  return static_cast<float>(static_cast<__bf16>(v));
+}
+
 constexpr int kFbBuckets = 16;
 struct FbLists {
   int2* list;
@@ -889,7 +900,7 @@ __device__ __forceinline__ void gate_tile(
         // + 0: a key of -0 ranks as +0 (they are equal keys). Clamped to
         // -+0x1.fep127, whose low 16 bits are zero, so that the low bits
         // keep it a number (a masked group: "none").
-        const float kr = fminf(fmaxf(Elem<T>::round(mx + widen(mx)) + 0.f, -0x1.fep127f), 0x1.fep127f);
+        const float kr = fminf(fmaxf(key_round<T>(mx + widen(mx)) + 0.f, -0x1.fep127f), 0x1.fep127f);
         const uint32_t g = kr < 0.f ? static_cast<uint32_t>(gid) : static_cast<uint32_t>(max_gid - gid);
         key = __uint_as_float(__float_as_uint(kr) | (g << SLOT_BITS) | slot);
       } else {
@@ -992,7 +1003,7 @@ __device__ __forceinline__ void gate_tile(
     // below the midpoint between kt0 and the key under it (less a margin
     // of two widths) round below kt0 and cannot be needed.
     if (tau > -INFINITY) {
-      const float kt0 = Elem<T>::round(tau - widen(tau));
+      const float kt0 = key_round<T>(tau - widen(tau));
       const float mid = 0.5f * (kt0 + key_below<T>(kt0));
       theta = nextafterf(mid - 2.f * widen(mid), -INFINITY);
     }
@@ -1065,7 +1076,7 @@ __device__ __forceinline__ void gate_tile(
       float kl[TS];
 #pragma unroll
       for (int p = 0; p < TS; ++p) kl[p] = -INFINITY;
-      auto lower = [&](float x) { return x > -INFINITY ? Elem<T>::round(x - widen(x)) : -INFINITY; };
+      auto lower = [&](float x) { return x > -INFINITY ? key_round<T>(x - widen(x)) : -INFINITY; };
       const float kinf = opaque_inf();
 #pragma unroll
       for (int p = 0; p < M; ++p) insert_value<TS>(kl, lower(half == 0 ? lv[p] : pv[p]), kinf);
@@ -1084,9 +1095,9 @@ __device__ __forceinline__ void gate_tile(
       auto visit = [&](float x, int j) {
         if (!(x > -INFINITY)) return;
         const float w = widen(x);
-        const float khi = Elem<T>::round(x + w);
+        const float khi = key_round<T>(x + w);
         if (khi < Lk) return;
-        const float klo = Elem<T>::round(x - w);
+        const float klo = key_round<T>(x - w);
         if (klo == khi) {
           insert_exact<TS>(fv, fi, klo, j);
         } else {
@@ -1136,7 +1147,7 @@ __device__ __forceinline__ void gate_tile(
         it = p == take - 1 ? fi[p] : it;
       }
       // Scores below theta have keys below every selected key.
-      if (theta > -INFINITY && !(kt > Elem<T>::round(theta + widen(theta)))) ok = false;
+      if (theta > -INFINITY && !(kt > key_round<T>(theta + widen(theta)))) ok = false;
       // What the lists left out must rank below the take-th selected.
       if (rk_m > kt || (rk_m == kt && rid_m < it)) ok = false;
       if (rk_p > kt || (rk_p == kt && rid_p < it)) ok = false;
@@ -1195,8 +1206,8 @@ __device__ __forceinline__ void gate_tile(
     const int gx = FB ? keyed_gid(__uint_as_float(gu)) : static_cast<int>((gu & low_mask) >> SLOT_BITS);
     jx = gx * 2 * GB + 8 * hh + 4 * half + static_cast<int>(ix & 3);
     const float wd = widen_c(x);
-    klo = Elem<T>::round(x - wd);
-    khi = Elem<T>::round(x + wd);
+    klo = key_round<T>(x - wd);
+    khi = key_round<T>(x + wd);
   };
   if ((!FB || keyed) && n_chunks > 0 && live && take > 0) {
 #pragma unroll
@@ -1306,7 +1317,7 @@ __device__ __forceinline__ void gate_tile(
     const float rej = fmaxf(rej_mine, __shfl_xor(rej_mine, 32));
     const float U = fmaxf(rej, theta);
     if (!FB && ok && take > 0 && live && U > -INFINITY) {
-      const float Uk = Elem<T>::round(U + widen(U));
+      const float Uk = key_round<T>(U + widen(U));
       float kt = -INFINITY;
 #pragma unroll
       for (int p = 0; p < TS; ++p) kt = p == take - 1 ? fv[p] : kt;
@@ -1325,7 +1336,7 @@ __device__ __forceinline__ void gate_tile(
         kt = p == take - 1 ? fv[p] : kt;
         it = p == take - 1 ? fi[p] : it;
       }
-      if (U > -INFINITY && !(kt > Elem<T>::round(U + widen(U)))) ok = false;
+      if (U > -INFINITY && !(kt > key_round<T>(U + widen(U)))) ok = false;
       const float evk = keyed_val(ev);
       const int ev_lo = evk > -INFINITY ? keyed_gid(ev) * 2 * GB + 4 * half : 0x7fffffff;
       const bool mine = !(evk > kt) && !(evk == kt && ev_lo <= it);
@@ -1349,7 +1360,7 @@ __device__ __forceinline__ void gate_tile(
     auto fold = [&]() {
       for (int e = 0; e < cnt; ++e) {
         const float x = sv[e * 64];
-        insert_keyed<M>(lk, lv, li, Elem<T>::round(x + widen(x)), x, si[e * 64]);
+        insert_keyed<M>(lk, lv, li, key_round<T>(x + widen(x)), x, si[e * 64]);
       }
       cnt = 0;
       // A full list takes a later score only if it can beat the last entry.
