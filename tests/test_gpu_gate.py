@@ -283,15 +283,18 @@ def _heavy_tie_keys(shape, dtype, seed, device):
     return k.to(dtype).to(device)
 
 
-@pytest.mark.parametrize("case", ["packed_gqa", "d128", "take16_bs32", "multi_tile_lists"])
+@pytest.mark.parametrize("case", ["packed_gqa", "d128", "take16_bs32", "multi_tile_lists",
+                                  "append_wide_ids"])
 def test_gate_fallback_kernel_paths_match_oracle(device, case):
     """Shared-offset keys leave many queries of a workgroup unsettled, so the
     first kernel hands them to the fallback kernel (its tile counter is
     non-zero): through packed sequences with grouped query heads, at head
-    dim 128 (where every unsettled query goes there), at take 16 with
-    32-key blocks, and with lists long enough that several tiles of one
-    list are spread over the workgroups striding over it. Every id as the
-    oracle selects it."""
+    dim 128, at take 16 with 32-key blocks, with lists long enough that
+    several tiles of one list are spread over the workgroups striding over
+    it, and with more groups than a float16 key's 13 free low bits can name
+    next to a slot (8192 blocks at take 16), where the fallback kernel
+    appends scores to lists instead of tracking keyed groups. Every id as
+    the oracle selects it (every fourth query in the last case)."""
     dtype = torch.bfloat16
     cu = mx = None
     if case == "packed_gqa":
@@ -311,15 +314,24 @@ def test_gate_fallback_kernel_paths_match_oracle(device, case):
         cfg = MoBAConfig(block_size=32, top_k=17, dtype=dtype)
         q = make_qkv((1, 8192, 2, 64), dtype, seed=45, device=device, n=1)[0]
         k = _heavy_tie_keys((1, 8192, 2, 64), dtype, 46, device)
-    else:
+    elif case == "multi_tile_lists":
         cfg = MoBAConfig(block_size=64, top_k=8, dtype=dtype)
         q = make_qkv((1, 65536, 2, 64), dtype, seed=47, device=device, n=1)[0]
         k = _heavy_tie_keys((1, 65536, 2, 64), dtype, 48, device)
+    else:
+        dtype = torch.float16
+        cfg = MoBAConfig(block_size=16, top_k=17, dtype=dtype)
+        q = make_qkv((1, 131072, 2, 64), dtype, seed=49, device=device, n=1)[0]
+        k = _heavy_tie_keys((1, 131072, 2, 64), dtype, 50, device)
     kbar = pool_blocks(k, cfg, cu_seqlens=cu, max_seqlen=mx)
     got, queued, tiles = _gate_with_counters(q, kbar, cfg, cu, mx)
     print(f"[fallback paths] {case}: fallback tiles {tiles}, queued {queued}", flush=True)
-    ref = c_oracle.gate_select(q.cpu(), kbar.cpu(), oracle_cfg(cfg),
-                               None if cu is None else cu.cpu(), mx)
+    if case == "append_wide_ids":
+        ref = c_oracle.gate_select_strided(q.cpu(), kbar.cpu(), oracle_cfg(cfg), stride=4)
+        got = got[:, :, ::4]
+    else:
+        ref = c_oracle.gate_select(q.cpu(), kbar.cpu(), oracle_cfg(cfg),
+                                   None if cu is None else cu.cpu(), mx)
     bad = (got.cpu() != ref).any(-1)
     assert not bool(bad.any()), (
         f"{int(bad.sum())} queries route differently; first {torch.nonzero(bad)[0].tolist()}")
