@@ -391,17 +391,18 @@ gate_exact_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
 }
 
 // ---------------------------------------------------------------------------
-// Queue kernel: one wave per queued query, four queries per workgroup. The
-// lanes split the query's candidates, each keeps an exact top-T list, and
-// the lists merge with a butterfly over the wave. Queries reach the queue
-// when the MFMA kernel's evidence cannot settle them: rarely for
-// independent keys, by the thousands for keys whose representatives nearly
-// coincide (many equal rounded scores), so the kernel is laid out for
-// throughput: no workgroup barriers, and each lane requests the rows of U
+// Queue kernel: one workgroup of kQueueWaves waves per queued query. The
+// lanes split the query's candidates, each keeps an exact top-T list, the
+// lists merge with a butterfly over each wave, and wave 0 merges the waves'
+// lists through LDS. Queries reach the queue when the MFMA kernel's evidence
+// cannot settle them: a few dozen for random-walk or offset keys at 512K,
+// by the thousands for constructed ties. With a few, the kernel is the
+// gate's tail: one wave per query (the earlier layout) scanned a late
+// query's ~4096 blocks alone for ~86 us. Each lane requests the rows of U
 // blocks before it scores any of them (float64 products and sum, as
 // exact_score), with the query row in registers.
 // ---------------------------------------------------------------------------
-constexpr int kQueueWaves = 4;
+constexpr int kQueueWaves = 8;
 
 template <typename T, int TMAX, int D>
 __global__ void __launch_bounds__(64 * kQueueWaves)
@@ -412,11 +413,15 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
                   const int64_t* __restrict__ queue, const int* __restrict__ queue_len) {
   constexpr int U = 256 / D;  // rows in flight per lane
   constexpr int C = D / 8;     // 16-byte chunks per row
+  constexpr int NL = 64 * kQueueWaves;  // lanes per query
+  __shared__ float s_val[kQueueWaves][TMAX];
+  __shared__ int s_idx[kQueueWaves][TMAX];
   const int lane = threadIdx.x & 63;
-  const int64_t total = *queue_len;
+  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int64_t total = *queue_len;  // uniform: every wave runs the same items
   const bool packed = cu != nullptr;
-  const int64_t first = static_cast<int64_t>(blockIdx.x) * kQueueWaves + (threadIdx.x >> 6);
-  for (int64_t item = first; item < total; item += static_cast<int64_t>(gridDim.x) * kQueueWaves) {
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
     const int64_t code = queue[item];  // (r * h_q + hq) * rows_per_seq + t
     const int64_t t = code % rows_per_seq;
     const int64_t rh = code / rows_per_seq;
@@ -433,7 +438,7 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
     if constexpr (Elem<T>::kCode == MOBA_FP16) {
       // fp16's software conversion needs the registers: one candidate at a
       // time per lane.
-      for (int j = lane; j < own; j += 64) {
+      for (int j = tid; j < own; j += NL) {
         const float sc = exact_score(qrow, kb + static_cast<int64_t>(j) * D, D);
         if (ranks_before(sc, j, val[take - 1], idx[take - 1])) insert_exact<TMAX>(val, idx, sc, j);
       }
@@ -441,18 +446,18 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       uint4 qv[C];
 #pragma unroll
       for (int c = 0; c < C; ++c) qv[c] = *reinterpret_cast<const uint4*>(qrow + 8 * c);
-      for (int j0 = lane; j0 < own; j0 += U * 64) {
+      for (int j0 = tid; j0 < own; j0 += U * NL) {
         uint4 kv[U][C];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int j = j0 + u * 64;
+          const int j = j0 + u * NL;
           const T* krow = kb + static_cast<int64_t>(j < own ? j : 0) * D;
 #pragma unroll
           for (int c = 0; c < C; ++c) kv[u][c] = *reinterpret_cast<const uint4*>(krow + 8 * c);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int j = j0 + u * 64;
+          const int j = j0 + u * NL;
           double acc = 0.0;
 #pragma unroll
           for (int c = 0; c < C; ++c) {
@@ -483,14 +488,36 @@ gate_queue_kernel(const T* __restrict__ q, const T* __restrict__ kbar,
       }
       merge_top<TMAX>(val, idx, pv, pi);
     }
+    // Every lane of a wave holds the wave's list; wave 0 merges the others'.
     if (lane == 0) {
-      int n_sel = 0;
 #pragma unroll
-      for (int p = 0; p < TMAX; ++p)
-        if (p < take && val[p] > -INFINITY) n_sel = p + 1;
-      emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
-                        out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
+      for (int p = 0; p < TMAX; ++p) {
+        s_val[wave][p] = val[p];
+        s_idx[wave][p] = idx[p];
+      }
     }
+    __syncthreads();
+    if (wave == 0) {
+      for (int w = 1; w < kQueueWaves; ++w) {
+        float pv[TMAX];
+        int pi[TMAX];
+#pragma unroll
+        for (int p = 0; p < TMAX; ++p) {
+          pv[p] = s_val[w][p];
+          pi[p] = s_idx[w][p];
+        }
+        merge_top<TMAX>(val, idx, pv, pi);
+      }
+      if (lane == 0) {
+        int n_sel = 0;
+#pragma unroll
+        for (int p = 0; p < TMAX; ++p)
+          if (p < take && val[p] > -INFINITY) n_sel = p + 1;
+        emit_sorted<TMAX>(idx, n_sel, own, cur != 0,
+                          out + hm_query(packed, r, hq, h_q, S, tok, t) * slots, slots);
+      }
+    }
+    __syncthreads();  // the lists of this item are read before the next is written
   }
 }
 
@@ -1717,7 +1744,7 @@ static int run_gate(const void* q, const void* kbar, int32_t* out, const int32_t
   }
   if (rc) return rc;
   // Queries whose approximate evidence was insufficient: exact rescoring,
-  // one wave per query.
+  // one workgroup per query.
   auto queue_launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(1024), dim3(64 * kQueueWaves), 0, st, static_cast<const T*>(q),
                        static_cast<const T*>(kbar), out, cu, g.seq_len, g.rows_per_seq, g.h_q,
