@@ -28,9 +28,8 @@
 //     what D float32 additions, each rounding by at most one ulp, can
 //     lose) plus the denormal terms, so a score's key (the exact score
 //     rounded to float32 and to the dtype) lies in [R(a - w), R(a + w)], w
-//     being E
-//     widened by float32 rounding. The candidates (scores >= theta of the
-//     kept groups) are compacted per lane; those with a single possible
+//     being E widened by float32 rounding. The candidates (scores >= theta
+//     of the kept groups) are compacted per lane; those with a single possible
 //     key are ranked by it, those straddling a rounding boundary and not
 //     below the take-th lower key bound are rescored exactly (float64
 //     partial dots of the two lanes, rounded like the oracle). The result
@@ -38,9 +37,7 @@
 //     below theta, candidates beyond the buffers) has a key bound strictly
 //     below the take-th selected key.
 //   - Unsettled queries go, with their theta, to lists per (row, query
-//     head, position bucket) for the fallback kernel. (A second stream in
-//     the workgroup itself for up to 4 of them, the earlier design, cost
-//     offset keys 0.2 ms for 0.02 ms on i.i.d. keys.)
+//     head, position bucket) for the fallback kernel.
 //
 // * gate_fallback_kernel: tiles of 128 such queries stream every chunk up
 //   to the tile's horizon, with pass 1's group tracking, but the groups
@@ -53,14 +50,18 @@
 //   above the lane's threshold to a per-lane LDS buffer instead, folded
 //   into lists of the M best by (largest key, id).
 //   The work follows the number of unsettled queries, not the number of
-//   workgroups holding one.
+//   workgroups holding one. A list's last tile of at most 32 queries runs
+//   in a split launch instead: its four waves take the same queries and a
+//   quarter of the chunks each, and wave 0 merges their keyed lists, so a
+//   lone late tile does not stream alone at one wave per SIMD.
 //
 //   A query that settles nowhere (more straddling candidates than the
 //   buffers hold, constructed ties, inf / NaN input) is queued; it is
 //   never guessed.
 //
-// * gate_queue_kernel: one wave per queued query, exact scores for every
-//   candidate, lists merged across the wave.
+// * gate_queue_kernel: one workgroup of eight waves per queued query,
+//   exact scores for every candidate, lists merged across each wave and
+//   then across the waves.
 //
 // * gate_exact_kernel (fp32, take > 16 or unsupported shapes). One thread
 //   per query, exact float64 scores for every candidate, streaming top-T in
