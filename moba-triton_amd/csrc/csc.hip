@@ -15,8 +15,10 @@
 //
 // The order pass ranks each column directly -- rank = #columns with a larger
 // count, or the same count and a smaller id -- one lane per column against an
-// LDS copy of the counts. It is O(nb^2) work spread over nb lanes; at
-// nb = 4096 that is ~16M integer compares per head (28 us for four heads).
+// LDS copy of the counts (order_kernel): O(nb^2) work spread over nb lanes,
+// ~16M integer compares per head at nb = 4096 (27 us for four heads). From
+// 4097 to 16384 columns it sorts (count desc, id asc) keys per (row, kv head)
+// in LDS with a bitonic network instead (order_sort_kernel, O(nb log^2 nb)).
 #include <mutex>
 
 #include "common.h"
@@ -464,6 +466,45 @@ order_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ order,
   if (c < n_blocks && sub == 0) order[rh * n_blocks + rank] = static_cast<int32_t>(c);
 }
 
+// The same order by sorting: one workgroup per (row, kv head) sorts the
+// 64-bit keys (INT32_MAX - count) << 32 | id ascending -- count descending,
+// id ascending -- in LDS with a bitonic network over n2 keys (the power of
+// two >= n_blocks; the padding keys, all ones, sort last). O(n log^2 n)
+// against the rank kernel's O(n^2): 78 barrier-separated passes at
+// n_blocks = 4096, each lane comparing two pairs per pass. Dynamic LDS:
+// 8 * n2 bytes, so up to n2 = 16384 on a device with 160 KiB.
+constexpr int kOrderSortMaxKeys = 16384;
+constexpr size_t kOrderSortMaxLds = 8 * static_cast<size_t>(kOrderSortMaxKeys);
+__global__ void __launch_bounds__(1024)
+order_sort_kernel(const int32_t* __restrict__ col_nnz, int32_t* __restrict__ order,
+                  int64_t n_blocks, int n2) {
+  extern __shared__ uint64_t okey[];
+  const int64_t rh = blockIdx.x;
+  const int32_t* cnt = col_nnz + rh * n_blocks;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n2; i += 1024)
+    okey[i] = i < n_blocks
+                  ? (static_cast<uint64_t>(0x7fffffff - cnt[i]) << 32) | static_cast<uint32_t>(i)
+                  : ~uint64_t{0};
+  __syncthreads();
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < n2 / 2; i += 1024) {
+        const int lo = 2 * i - (i & (j - 1));  // pair (lo, lo + j), lo's bit j clear
+        const uint64_t x = okey[lo], y = okey[lo + j];
+        // Ascending where bit k of lo is clear, descending where it is set.
+        if ((x > y) == ((lo & k) == 0)) {
+          okey[lo] = y;
+          okey[lo + j] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int64_t i = tid; i < n_blocks; i += 1024)
+    order[rh * n_blocks + i] = static_cast<int32_t>(okey[i] & 0xffffffffu);
+}
+
 // Segment list of one (row, kv head): its columns in `order` (longest first),
 // a column of n entries cut into min(max_seg, ceil(n / seg_len)) segments of
 // near-equal length (at least one, also when empty). Entry (c, s, nseg, x):
@@ -532,9 +573,10 @@ UnitPlan unit_plan(int64_t rows_per_seq, int64_t h_q, int64_t h_kv, int64_t tq) 
   p.nchunks = moba::cdiv(p.units, p.chunk);
   return p;
 }
-// True when det_scatter_kernel may take `bytes` of dynamic LDS on the
-// current device: always up to 64 KiB; beyond that when the device's opt-in
-// limit allows it, after raising the kernel's limit once per process.
+// True when det_scatter_kernel (order_sort_kernel) may take `bytes` of
+// dynamic LDS on the current device: always up to 64 KiB; beyond that when
+// the device's opt-in limit allows it, after raising both kernels' limits
+// (to kDetLdsBytes, kOrderSortMaxLds) once per process.
 bool det_lds_ok(size_t bytes) {
   if (bytes <= 65536) return true;
   int dev = 0, optin = 0;
@@ -547,7 +589,10 @@ bool det_lds_ok(size_t bytes) {
   std::call_once(once, [] {
     raised = hipFuncSetAttribute(reinterpret_cast<const void*>(moba::det_scatter_kernel),
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 static_cast<int>(moba::kDetLdsBytes)) == hipSuccess;
+                                 static_cast<int>(moba::kDetLdsBytes)) == hipSuccess &&
+             hipFuncSetAttribute(reinterpret_cast<const void*>(moba::order_sort_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(moba::kOrderSortMaxLds)) == hipSuccess;
   });
   return raised;
 }
@@ -660,8 +705,16 @@ extern "C" int moba_csc_build(const int32_t* block_idx, int32_t* col_nnz,
                        nullptr, index_stride);
   }
   hipLaunchKernelGGL(scan_kernel, dim3(rhk), dim3(1024), 0, s, col_nnz, col_offsets, n_blocks);
-  hipLaunchKernelGGL(order_kernel, dim3(static_cast<unsigned>(cdiv(n_blocks, 32)), rhk),
-                     dim3(256), 0, s, col_nnz, order, n_blocks);
+  int n2 = 1;
+  while (n2 < n_blocks) n2 <<= 1;
+  // The rank kernel is faster up to 4096 columns (27 vs 36 us for four
+  // heads at 4096); its O(nb^2) cost passes the sort's above.
+  if (n_blocks > 4096 && n2 <= kOrderSortMaxKeys && det_lds_ok(8 * static_cast<size_t>(n2)))
+    hipLaunchKernelGGL(order_sort_kernel, dim3(rhk), dim3(1024), 8 * static_cast<unsigned>(n2), s,
+                       col_nnz, order, n_blocks, n2);
+  else
+    hipLaunchKernelGGL(order_kernel, dim3(static_cast<unsigned>(cdiv(n_blocks, 32)), rhk),
+                       dim3(256), 0, s, col_nnz, order, n_blocks);
   if (segments)
     hipLaunchKernelGGL(seg_build_kernel, dim3(rhk), dim3(1024), 0, s, col_nnz, order, n_blocks,
                        seg_len, static_cast<int>(max_seg), segments, seg_split, seg_counts,

@@ -207,6 +207,11 @@ def test_csc_column_order(device, s, nb, packed, slots):
     want = canonical(idx, nb, h_kv, cu)
     for (r, kv), w in want.items():
         assert torch.equal(entries(got, r, kv), w), (r, kv)
+    # Longest column first, ties by ascending id (routing.py:548-553); above
+    # 4096 columns the build sorts, below it ranks.
+    nnz = got.col_nnz.long().cpu()
+    want_order = torch.argsort(-nnz, dim=-1, stable=True).to(torch.int32)
+    assert torch.equal(got.order.cpu(), want_order)
 
 
 def test_gradients_are_bitwise_stable_across_index_builds(device):
