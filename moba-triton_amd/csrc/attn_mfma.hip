@@ -425,6 +425,15 @@ int attend_mfma(const AttnArgs& a, int dtype, int acc_dtype, int64_t n_cols, hip
 // inside the workgroup, so the partial buffer is [.., slots, D], not
 // slots x sub-tiles. Semantics: src/moba/kernels/moba_bwd.py:216-394.
 // ---------------------------------------------------------------------------
+// Piece permutation of a Q / dO tile row (bwd_mfma_kernel at head_dim 64):
+// bits 1-3 of the row, reversed. Rows 2i and 2i + 1 share it; the eight
+// even (odd) rows of 16 consecutive ones take eight distinct values, and
+// rows 4a, 4a + 1 and 4a + 2, 4a + 3 differ in bit 2, which moves a
+// 64-byte run of four pieces to the other half of the row.
+__device__ constexpr int bq_swz(int row) {
+  return (((row >> 1) & 1) << 2) | ((row >> 1) & 2) | ((row >> 3) & 1);
+}
+
 template <typename T, typename A, int D, int BS, int NQ, int ST>
 __global__ void __launch_bounds__(BS * 2 * ST, (D == 64 && BS == 128) ? 2 : 1)
 bwd_mfma_kernel(AttnArgs a) {
@@ -445,6 +454,18 @@ bwd_mfma_kernel(AttnArgs a) {
   constexpr bool kKV = ST > 1;
   constexpr int DT = D / 32;
   constexpr int RS = D + 8;     // row stride of [key|q][d] tiles
+  // Q / dO tiles at head_dim 64 with one stream: unpadded 128-byte rows
+  // whose 16-byte pieces are permuted by bq_swz (qx below). The S / dP row
+  // reads (16 lanes: 16 consecutive rows, one piece each) and the
+  // transposing reads (32 lanes: 4 consecutive rows x 4 pieces) then meet
+  // 16 distinct 4-bank groups per 16 lanes; with the padded stride the
+  // transposing reads folded rows r and r + 2 onto the same banks. Each
+  // lane's addresses stay loop-invariant.
+  constexpr bool kSwz = D == 64 && !kKV;
+  constexpr int QRS = kSwz ? D : RS;  // row stride of the Q / dO tiles
+  auto qx = [](int row, int e) {      // element offset of (row, feature e)
+    return kSwz ? row * QRS + ((((e >> 3) ^ bq_swz(row)) << 3) | (e & 7)) : row * QRS + e;
+  };
   constexpr int KTS = BS + 8;   // row stride of K^T ([d][key])
   // Row stride of dS^T ([key][q]): 34 banks, so the 32 keys of a wave's
   // 8-byte dS writes land on distinct bank pairs (NQ + 8 paired keys c and
@@ -454,7 +475,7 @@ bwd_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Kl[kKV ? 2 * BS * RS : D * KTS];
   // Per stream: Q rows, dO rows, dS^T. One array, so that the float32
   // hand-over of dK / dV between the streams can reuse all of it.
-  constexpr int kRows = 2 * NQ * RS + BS * QS2;
+  constexpr int kRows = 2 * NQ * QRS + BS * QS2;
   __shared__ __attribute__((aligned(16))) uint16_t Sm[ST * kRows];
   __shared__ __attribute__((aligned(16))) float s_lse_[ST][NQ];
   __shared__ __attribute__((aligned(16))) float s_delta_[ST][NQ];
@@ -467,7 +488,7 @@ bwd_mfma_kernel(AttnArgs a) {
   constexpr int TPW = DT * (NQ / 32) / (BS / 32);
   constexpr int DQS = 40;
   __shared__ __attribute__((aligned(16))) uint16_t DQs_[sizeof(A) == 2 ? ST * (BS / 32) * TPW * 32 * DQS : 8];
-  static_assert((NQ * RS * 2) % 16 == 0 && (kRows * 2) % 16 == 0, "16-byte aligned carving");
+  static_assert((NQ * QRS * 2) % 16 == 0 && (kRows * 2) % 16 == 0, "16-byte aligned carving");
 
   const Column c = resolve_column(a, blockIdx.x, blockIdx.y);
   if (c.skip) return;  // past the segment list (uniform)
@@ -486,8 +507,8 @@ bwd_mfma_kernel(AttnArgs a) {
   const int stid = kKV ? tid % NT : tid;  // thread index within the stream
   const int wave = stid >> 6;
   uint16_t* Qs = Sm + stream * kRows;
-  uint16_t* Os = Qs + NQ * RS;
-  uint16_t* DSt = Os + NQ * RS;
+  uint16_t* Os = Qs + NQ * QRS;
+  uint16_t* DSt = Os + NQ * QRS;
   uint16_t* Kt = Kl;          // one stream
   uint16_t* Ks = Kl;          // two streams
   uint16_t* Vs = kKV ? Kl + BS * RS : Kl;  // (unused with one stream)
@@ -634,8 +655,8 @@ bwd_mfma_kernel(AttnArgs a) {
       const int i = stid + u * NT;
       const int q = i / (D / 8);
       const int d8 = (i % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&Qs[q * RS + d8]) = pv[u] && act ? pq[u] : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&Os[q * RS + d8]) = pv[u] && act ? po[u] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Qs[qx(q, d8)]) = pv[u] && act ? pq[u] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Os[qx(q, d8)]) = pv[u] && act ? po[u] : u32x4{0, 0, 0, 0};
     }
   };
   // vmcnt(0): the K / V operands and the prologue loads are all resident, so
@@ -676,16 +697,15 @@ bwd_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       floatx16_t sacc = floatx16_t{}, pacc = floatx16_t{};
-      const uint16_t* qa = &Qs[(qt * 32 + col) * RS + 8 * h];
-      const uint16_t* oa = &Os[(qt * 32 + col) * RS + 8 * h];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
+        const int qo = qx(qt * 32 + col, 16 * k + 8 * h);
         if constexpr (kKV) {
-          sacc = M::mma(ld16<V8>(qa + 16 * k), ld16<V8>(&Ks[mykey * RS + 16 * k + 8 * h]), sacc);
-          pacc = M::mma(ld16<V8>(oa + 16 * k), ld16<V8>(&Vs[mykey * RS + 16 * k + 8 * h]), pacc);
+          sacc = M::mma(ld16<V8>(&Qs[qo]), ld16<V8>(&Ks[mykey * RS + 16 * k + 8 * h]), sacc);
+          pacc = M::mma(ld16<V8>(&Os[qo]), ld16<V8>(&Vs[mykey * RS + 16 * k + 8 * h]), pacc);
         } else {
-          sacc = M::mma(ld16<V8>(qa + 16 * k), kb[k], sacc);
-          pacc = M::mma(ld16<V8>(oa + 16 * k), vb[k], pacc);
+          sacc = M::mma(ld16<V8>(&Qs[qo]), kb[k], sacc);
+          pacc = M::mma(ld16<V8>(&Os[qo]), vb[k], pacc);
         }
       }
       V8 pb[2], db[2];  // P and dS as B operands, K-steps over queries
@@ -734,9 +754,10 @@ bwd_mfma_kernel(AttnArgs a) {
       for (int j = 0; j < 2; ++j) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const int o0 = (qt * 32 + 16 * j + tr_row) * RS + dt * 32 + tr_col;
-          dv[dt] = M::mma(ld_tr2<V8>(&Os[o0], &Os[o0 + 8 * RS]), pb[j], dv[dt]);
-          dk[dt] = M::mma(ld_tr2<V8>(&Qs[o0], &Qs[o0 + 8 * RS]), db[j], dk[dt]);
+          const int o0 = qx(qt * 32 + 16 * j + tr_row, dt * 32 + tr_col);
+          const int o1 = qx(qt * 32 + 16 * j + tr_row + 8, dt * 32 + tr_col);
+          dv[dt] = M::mma(ld_tr2<V8>(&Os[o0], &Os[o1]), pb[j], dv[dt]);
+          dk[dt] = M::mma(ld_tr2<V8>(&Qs[o0], &Qs[o1]), db[j], dk[dt]);
         }
       }
     }
